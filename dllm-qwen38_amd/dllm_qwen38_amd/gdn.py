@@ -1,0 +1,358 @@
+"""Gated DeltaNet forward with per-chunk states and the state fork, on MI355X HIP kernels.
+
+Drop-in for the reference's `src/dllm_qwen38/gdn.py` entry points:
+  chunk_gated_delta_rule_with_states (gdn.py:48-123), set_impl / last_impl (gdn.py:39-45),
+  gdn_mixer_forward (gdn.py:193-233), plus the conv seam causal_conv1d_fn
+  (transformers modeling_qwen3_5.py:219-239) and the fused two-stream fork op used by
+  `blockdiff.block_diffusion_forward` (reference blockdiff.py:153-177).
+
+Every core runs the hand-written gfx950 kernels of libdllm_hip.so through its C ABI. There is no
+CPU or torch implementation behind these functions: a CPU tensor, a missing library or a kernel
+error raises. GQA is handled by indexing the key head (value head j reads key head j // (Hv/Hk));
+q/k are never expanded.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+# Which core the last call used and why — reports name the path they measured (gdn.py:22-24).
+_IMPL = {"force": None, "last": "hip", "reason": ""}
+
+
+def set_impl(name):
+    """'hip' | None. The reference also accepts 'torch' / 'fla'; this build has only the HIP core,
+    so forcing anything else raises (gdn.py:39-41, 158-159)."""
+    if name not in (None, "hip"):
+        raise RuntimeError(f"{name} forced but unavailable: this build runs the HIP core only")
+    _IMPL["force"] = name
+
+
+def last_impl():
+    return _IMPL["last"], _IMPL["reason"]
+
+
+def _fp32c(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.float32).contiguous()
+
+
+def _lastdim_contig(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def chunk_gated_delta_rule_with_states(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    chunk_size: int,
+    initial_state: torch.Tensor | None = None,
+    use_qk_l2norm_in_kernel: bool = True,
+    need_states: bool = True,
+):
+    """Return (core_attn_out [B, T, Hv, Dv], states [B, n_chunks, Hv, Dk, Dv] fp32 or None).
+
+    Same contract as the reference (gdn.py:48-123): states[:, i] is the recurrent state after
+    chunk i; T must be a multiple of chunk_size (ValueError otherwise). q/k may carry Hk <= Hv
+    heads (Hv % Hk == 0) in addition to the reference's already-expanded layout."""
+    dev = _lib.require_device(query, key, value, g, beta, initial_state)
+    if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+        raise ValueError("query/key/value must be [B, T, H, D]")
+    B, T, Hk, Dk = key.shape
+    Hv, Dv = value.shape[-2:]
+    if query.shape != key.shape:
+        raise ValueError(f"query {tuple(query.shape)} and key {tuple(key.shape)} differ")
+    if value.shape[:2] != (B, T):
+        raise ValueError("value must share [B, T] with key")
+    if T % chunk_size != 0:
+        raise ValueError(f"sequence_length {T} is not a multiple of chunk_size {chunk_size}")
+    if Hv % Hk:
+        raise ValueError(f"num value heads {Hv} is not a multiple of num key heads {Hk}")
+    dt = query.dtype
+    if key.dtype != dt or value.dtype != dt:
+        raise TypeError(f"query/key/value dtypes differ ({dt}, {key.dtype}, {value.dtype})")
+    code = _lib.dtype_code(dt)
+    q, k, v = _lastdim_contig(query), _lastdim_contig(key), _lastdim_contig(value)
+    gg, bb = _fp32c(g), _fp32c(beta)
+    if gg.shape != (B, T, Hv) or bb.shape != (B, T, Hv):
+        raise ValueError(f"g and beta must be [B, T, Hv] = {(B, T, Hv)}")
+    init = None
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (B, Hv, Dk, Dv):
+            raise ValueError(f"initial_state must be {(B, Hv, Dk, Dv)}, got {tuple(initial_state.shape)}")
+        init = _fp32c(initial_state)
+    out = torch.empty(B, T, Hv, Dv, dtype=dt, device=dev)
+    states = (torch.empty(B, T // chunk_size, Hv, Dk, Dv, dtype=torch.float32, device=dev)
+              if need_states else None)
+    L = _lib.lib()
+    _lib.check(L.dllm_gdn_chunk_fwd(
+        q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
+        gg.data_ptr(), _lib.strides3(gg), bb.data_ptr(), _lib.strides3(bb), _lib.ptr(init), out.data_ptr(),
+        _lib.ptr(states), B, T, Hk, Hv, Dk, Dv, chunk_size, code, int(bool(use_qk_l2norm_in_kernel)),
+        Dk ** -0.5, _lib.stream_handle(dev)), "dllm_gdn_chunk_fwd")
+    _IMPL["last"], _IMPL["reason"] = "hip", ""
+    return out, states
+
+
+def _core(q, k, v, g, beta, *, chunk_size, initial_state, need_states):
+    """Core dispatch (reference gdn.py:147-163): the HIP kernel; forcing another impl raises."""
+    if _IMPL["force"] not in (None, "hip"):
+        raise RuntimeError(f"{_IMPL['force']} forced but unavailable")
+    return chunk_gated_delta_rule_with_states(q, k, v, g, beta, chunk_size=chunk_size, initial_state=initial_state,
+                                              use_qk_l2norm_in_kernel=True, need_states=need_states)
+
+
+def causal_conv1d_fn(hidden_states: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                     activation: str | None = None, *, conv_prefix: torch.Tensor | None = None, **kwargs):
+    """Causal depthwise conv [B, C, T] -> [B, C, T] (transformers modeling_qwen3_5.py:219-239), with
+    an optional [B, C, P] prefix: equal to the conv over cat([prefix, x]) cut to the last T outputs
+    (reference gdn.py:217-219). The result is a [B, C, T] view of token-major [B, T, C] storage."""
+    if activation not in (None, "silu", "swish"):
+        raise ValueError(f"activation {activation} not supported (silu or None)")
+    dev = _lib.require_device(hidden_states, weight, bias, conv_prefix)
+    B, C, T = hidden_states.shape
+    K = weight.shape[-1]
+    w = weight.reshape(C, K).contiguous()
+    b = None if bias is None else bias.contiguous()
+    x = hidden_states
+    y = torch.empty(B, T, C, dtype=x.dtype, device=dev)
+    pre = conv_prefix
+    if pre is not None and (pre.shape[0] != B or pre.shape[1] != C):
+        raise ValueError(f"conv_prefix must be [B, C, P] = [{B}, {C}, P], got {tuple(pre.shape)}")
+    L = _lib.lib()
+    _lib.check(L.dllm_causal_conv1d_fwd(
+        x.data_ptr(), _lib.strides3(x), _lib.ptr(pre), None if pre is None else _lib.strides3(pre),
+        0 if pre is None else pre.shape[2], w.data_ptr(), _lib.ptr(b), y.data_ptr(), B, C, T, K,
+        _lib.dtype_code(x.dtype), _lib.dtype_code(w.dtype), int(activation is not None), _lib.stream_handle(dev)),
+        "dllm_causal_conv1d_fwd")
+    return y.transpose(1, 2)
+
+
+def _beta_g(m, b: torch.Tensor, a: torch.Tensor):
+    """beta = sigmoid(b) in the projection dtype; g = -exp(A_log) * softplus(a + dt_bias) in fp32
+    (reference gdn.py:225-226)."""
+    beta = b.sigmoid()
+    g = -m.A_log.float().exp() * F.softplus(a.float() + m.dt_bias)
+    return beta, g
+
+
+def _split_qkv(mixed: torch.Tensor, m, B: int, T: int):
+    """Views (no copies) of q [B,T,Hk,Dk], k, v [B,T,Hv,Dv] inside token-major [B,T,conv_dim]."""
+    kd, vd = m.key_dim, m.value_dim
+    q = mixed[..., :kd].unflatten(-1, (m.num_k_heads, m.head_k_dim))
+    k = mixed[..., kd: 2 * kd].unflatten(-1, (m.num_k_heads, m.head_k_dim))
+    v = mixed[..., 2 * kd: 2 * kd + vd].unflatten(-1, (m.num_v_heads, m.head_v_dim))
+    return q, k, v
+
+
+def gdn_mixer_forward(
+    m,
+    hidden_states: torch.Tensor,
+    *,
+    chunk_size: int,
+    conv_prefix: torch.Tensor | None = None,
+    initial_state: torch.Tensor | None = None,
+    need_states: bool = True,
+):
+    """Run a Qwen3.5 Gated DeltaNet module `m` on hidden_states [B, T, D] (reference gdn.py:193-233).
+
+    conv_prefix: [B, conv_dim, K-1] pre-conv projections of the tokens before this segment, or None.
+    initial_state: [B, Hv, Dk, Dv] recurrent state before the segment, or None for zeros.
+    Returns (output [B, T, D], states [B, T/chunk, Hv, Dk, Dv] | None, raw_qkv [B, conv_dim, T])."""
+    B, T, _ = hidden_states.shape
+    raw = m.in_proj_qkv(hidden_states)  # [B, T, conv_dim]
+    z = m.in_proj_z(hidden_states).reshape(B, T, -1, m.head_v_dim)
+    beta, g = _beta_g(m, m.in_proj_b(hidden_states), m.in_proj_a(hidden_states))
+    mixed = causal_conv1d_fn(raw.transpose(1, 2), m.conv1d.weight.squeeze(1), m.conv1d.bias,
+                             activation=m.activation, conv_prefix=conv_prefix).transpose(1, 2)
+    q, k, v = _split_qkv(mixed, m, B, T)
+    core, states = _core(q, k, v, g, beta, chunk_size=chunk_size, initial_state=initial_state,
+                         need_states=need_states)
+    core = m.norm(core.reshape(-1, m.head_v_dim), z.reshape(-1, m.head_v_dim)).reshape(B, T, -1)
+    return m.out_proj(core), states, raw.transpose(1, 2)
+
+
+# ----------------------------------------------------------------------------------------------
+# Fused state fork of one GDN layer (both streams)
+# ----------------------------------------------------------------------------------------------
+def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Tensor,
+                   beta0: torch.Tensor, betat: torch.Tensor, g0: torch.Tensor, gt: torch.Tensor, *,
+                   num_k_heads: int, num_v_heads: int, head_k_dim: int, head_v_dim: int, block: int,
+                   conv_bias: torch.Tensor | None = None, need_states: bool = True,
+                   need_tails: bool = True, fault: str | None = None, out: dict | None = None):
+    """The state-fork GDN layer core on pre-conv projections of both streams
+    (reference blockdiff.py:153-177 with gdn.py:217-231, projections excluded).
+
+    raw0/rawt [B, L, conv_dim] (token-major, the in_proj_qkv output); beta*/g* [B, L, Hv];
+    conv_weight [conv_dim, K]. Returns dict(o0, ot [B, L, Hv, Dv], states [B, nb, Hv, Dk, Dv] fp32
+    or None, tails [B*nb, conv_dim, K-1] or None).
+
+    fault: None | "no-conv-prefix" (noised blocks' conv starts cold). `out` may pass preallocated
+    buffers (keys o0, ot, states, tails, y0, yt) to keep the call allocation-free."""
+    dev = _lib.require_device(raw0, rawt, conv_weight, beta0, betat, g0, gt, conv_bias)
+    if raw0.shape != rawt.shape or raw0.dim() != 3:
+        raise ValueError("raw0 and rawt must both be [B, L, conv_dim]")
+    B, L, Cd = raw0.shape
+    if L % block:
+        raise ValueError(f"L={L} is not a multiple of block={block}")
+    Hk, Hv, Dk, Dv = num_k_heads, num_v_heads, head_k_dim, head_v_dim
+    if Cd != 2 * Hk * Dk + Hv * Dv:
+        raise ValueError(f"conv_dim {Cd} != 2*Hk*Dk + Hv*Dv = {2 * Hk * Dk + Hv * Dv}")
+    if fault not in (None, "no-conv-prefix"):
+        raise ValueError(f"fault {fault!r} is not a fork-level fault")
+    nb = L // block
+    K = conv_weight.shape[-1]
+    dt = raw0.dtype
+    code = _lib.dtype_code(dt)
+    r0, rt = raw0.contiguous(), rawt.contiguous()
+    w = conv_weight.reshape(Cd, K).contiguous()
+    bufs = out or {}
+
+    def buf(name, shape, dtype):
+        t = bufs.get(name)
+        if t is None:
+            t = torch.empty(shape, dtype=dtype, device=dev)
+        elif tuple(t.shape) != tuple(shape) or t.dtype != dtype or not t.is_contiguous():
+            raise ValueError(f"buffer {name} must be contiguous {shape} {dtype}")
+        return t
+
+    y0 = buf("y0", (B, L, Cd), dt)
+    yt = buf("yt", (B, L, Cd), dt)
+    tails = buf("tails", (B * nb, Cd, K - 1), dt) if need_tails else None
+    o0 = buf("o0", (B, L, Hv, Dv), dt)
+    ot = buf("ot", (B, L, Hv, Dv), dt)
+    states = buf("states", (B, nb, Hv, Dk, Dv), torch.float32) if need_states else None
+    b0, bt_, gg0, ggt = (_fp32c(x) for x in (beta0, betat, g0, gt))
+    for name, x in (("beta0", b0), ("betat", bt_), ("g0", gg0), ("gt", ggt)):
+        if tuple(x.shape) != (B, L, Hv):
+            raise ValueError(f"{name} must be [B, L, Hv] = {(B, L, Hv)}")
+    Lb = _lib.lib()
+    sh = _lib.stream_handle(dev)
+    _lib.check(Lb.dllm_conv_fork_fwd(
+        r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(conv_bias), y0.data_ptr(), yt.data_ptr(),
+        _lib.ptr(tails), B, L, Cd, K, block, code, _lib.dtype_code(w.dtype), 1 if fault == "no-conv-prefix" else 0,
+        sh), "dllm_conv_fork_fwd")
+    if Lb.dllm_gdn_fused_fork_supported(Dk, block, code):
+        _lib.check(Lb.dllm_gdn_state_fork_fwd(
+            y0.data_ptr(), yt.data_ptr(), L * Cd, Cd, b0.data_ptr(), bt_.data_ptr(), gg0.data_ptr(), ggt.data_ptr(),
+            o0.data_ptr(), ot.data_ptr(), _lib.ptr(states), B, L, Hk, Hv, Dk, Dv, block, code, Dk ** -0.5, sh),
+            "dllm_gdn_state_fork_fwd")
+        _IMPL["last"], _IMPL["reason"] = "hip", ""
+    else:
+        # two-pass fork on the same HIP core: clean pass with states, then the B*nb noised rows
+        # relaunched from the shifted states (reference blockdiff.py:160-176)
+        class _Dims:
+            key_dim, value_dim = Hk * Dk, Hv * Dv
+            num_k_heads, num_v_heads, head_k_dim, head_v_dim = Hk, Hv, Dk, Dv
+
+        q0, k0, v0 = _split_qkv(y0, _Dims, B, L)
+        o0c, st0 = chunk_gated_delta_rule_with_states(q0, k0, v0, gg0, b0, block, need_states=True)
+        o0.copy_(o0c)
+        init = torch.cat([torch.zeros_like(st0[:, :1]), st0[:, :-1]], 1).reshape(B * nb, Hv, Dk, Dv)
+        qt, kt, vt = _split_qkv(yt.view(B * nb, block, Cd), _Dims, B * nb, block)
+        otc, _ = chunk_gated_delta_rule_with_states(
+            qt, kt, vt, ggt.view(B * nb, block, Hv), bt_.view(B * nb, block, Hv), block, initial_state=init,
+            need_states=False)
+        ot.copy_(otc.view(B, L, Hv, Dv))
+        if states is not None:
+            states.copy_(st0)
+        _IMPL["last"], _IMPL["reason"] = "hip", "two-pass fork (fused kernel does not take this shape)"
+    return {"o0": o0, "ot": ot, "states": states, "tails": tails, "y0": y0, "yt": yt}
+
+
+def fork_layout(B: int, L: int, block: int, width: int = 4, device="cuda"):
+    """Integer fork maps computed on the device by the kernels' own index functions
+    (reference blockdiff.py:161-173): row [B, nb], state_src [B*nb], prefix_pos [B*nb, width-1]."""
+    if L % block:
+        raise ValueError(f"L={L} is not a multiple of block={block}")
+    nb = L // block
+    dev = torch.device(device)
+    row = torch.empty(B * nb, dtype=torch.int32, device=dev)
+    src = torch.empty(B * nb, dtype=torch.int32, device=dev)
+    pre = torch.empty(B * nb, max(width - 1, 1), dtype=torch.int32, device=dev)
+    _lib.require_device(row)
+    _lib.check(_lib.lib().dllm_fork_layout(B, L, block, width, row.data_ptr(), src.data_ptr(), pre.data_ptr(),
+                                           _lib.stream_handle(dev)), "dllm_fork_layout")
+    return {"row": row.view(B, nb), "state_src": src, "prefix_pos": pre[:, : width - 1]}
+
+
+def layer_flops(B: int, L: int, Hv: int, Dk: int, Dv: int, chunk: int) -> int:
+    """Algorithmic flops of the state-fork layer's chunk contractions (both streams): per chunk and
+    value head 6*C*Dk*Dv + 8*C^2*Dk (clean) and 4*C*Dk*Dv + 8*C^2*Dk (noised)."""
+    C = chunk
+    per = (6 * C * Dk * Dv + 8 * C * C * Dk) + (4 * C * Dk * Dv + 8 * C * C * Dk)
+    return (B * L // C) * Hv * per
+
+
+def layer_bytes(B: int, L: int, Hk: int, Hv: int, Dk: int, Dv: int, chunk: int, esize: int = 2, K: int = 4) -> int:
+    """Algorithmic HBM bytes of the layer op (inputs read once, outputs written once): raw qkv of both
+    streams, beta (input dtype) and g (fp32) of both streams, both outputs, the per-chunk fp32
+    states and the conv tails."""
+    Cd = 2 * Hk * Dk + Hv * Dv
+    T = B * L
+    raw = 2 * T * Cd * esize
+    bg = 2 * T * Hv * (esize + 4)
+    o = 2 * T * Hv * Dv * esize
+    states = (T // chunk) * Hv * Dk * Dv * 4
+    tails = (T // chunk) * Cd * (K - 1) * esize
+    return raw + bg + o + states + tails
+
+
+
+class StateForkPlan:
+    """Pre-validated, pre-allocated state-fork layer launches for repeated calls on fixed shapes
+    (benchmarks, serving loops): run() enqueues the conv kernel and the fused fork kernel on the
+    current stream with no allocation and no host synchronisation. Inputs are the tensors given
+    at construction (their contents may be rewritten between runs)."""
+
+    def __init__(self, raw0, rawt, conv_weight, beta0, betat, g0, gt, *, num_k_heads, num_v_heads, head_k_dim,
+                 head_v_dim, block, need_states=True, need_tails=True):
+        dev = _lib.require_device(raw0, rawt, conv_weight, beta0, betat, g0, gt)
+        B, L, Cd = raw0.shape
+        self.dims = (B, L, Cd, num_k_heads, num_v_heads, head_k_dim, head_v_dim, block)
+        self.code = _lib.dtype_code(raw0.dtype)
+        if not _lib.lib().dllm_gdn_fused_fork_supported(head_k_dim, block, self.code):
+            raise ValueError("StateForkPlan needs a shape the fused fork kernel takes")
+        if not (raw0.is_contiguous() and rawt.is_contiguous()):
+            raise ValueError("raw0/rawt must be contiguous [B, L, conv_dim]")
+        self.raw0, self.rawt = raw0, rawt
+        self.w = conv_weight.reshape(Cd, -1).contiguous()
+        self.beta0, self.betat, self.g0, self.gt = (_fp32c(x) for x in (beta0, betat, g0, gt))
+        dt = raw0.dtype
+        nb = L // block
+        K = self.w.shape[1]
+        self.K = K
+        self.y0 = torch.empty(B, L, Cd, dtype=dt, device=dev)
+        self.yt = torch.empty(B, L, Cd, dtype=dt, device=dev)
+        self.tails = torch.empty(B * nb, Cd, K - 1, dtype=dt, device=dev) if need_tails else None
+        self.o0 = torch.empty(B, L, num_v_heads, head_v_dim, dtype=dt, device=dev)
+        self.ot = torch.empty_like(self.o0)
+        self.states = (torch.empty(B, nb, num_v_heads, head_k_dim, head_v_dim, dtype=torch.float32, device=dev)
+                       if need_states else None)
+        self.device = dev
+        self._lib = _lib.lib()
+
+    def run_conv(self, stream=None):
+        B, L, Cd, Hk, Hv, Dk, Dv, block = self.dims
+        sh = stream if stream is not None else _lib.stream_handle(self.device)
+        _lib.check(self._lib.dllm_conv_fork_fwd(
+            self.raw0.data_ptr(), self.rawt.data_ptr(), self.w.data_ptr(), None, self.y0.data_ptr(),
+            self.yt.data_ptr(), _lib.ptr(self.tails), B, L, Cd, self.K, block, self.code,
+            _lib.dtype_code(self.w.dtype), 0, sh), "dllm_conv_fork_fwd")
+
+    def run_core(self, stream=None):
+        B, L, Cd, Hk, Hv, Dk, Dv, block = self.dims
+        sh = stream if stream is not None else _lib.stream_handle(self.device)
+        _lib.check(self._lib.dllm_gdn_state_fork_fwd(
+            self.y0.data_ptr(), self.yt.data_ptr(), L * Cd, Cd, self.beta0.data_ptr(), self.betat.data_ptr(),
+            self.g0.data_ptr(), self.gt.data_ptr(), self.o0.data_ptr(), self.ot.data_ptr(), _lib.ptr(self.states),
+            B, L, Hk, Hv, Dk, Dv, block, self.code, Dk ** -0.5, sh), "dllm_gdn_state_fork_fwd")
+
+    def run(self, stream=None):
+        self.run_conv(stream)
+        self.run_core(stream)
+        _IMPL["last"], _IMPL["reason"] = "hip", ""

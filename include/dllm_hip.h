@@ -1,0 +1,115 @@
+/*
+ * dllm_hip.h — C ABI of the MI355X (gfx950) block-diffusion forward hot path.
+ *
+ * Conventions (every entry point):
+ *  - Tensor arguments are DEVICE pointers owned by the caller; sizes are plain ints; strides are
+ *    int64 element counts passed through small HOST arrays.
+ *  - `stream` is a hipStream_t (passed as void*); work is enqueued asynchronously on it and the
+ *    call never synchronises the device.
+ *  - dtype codes: 0 = float32, 1 = bfloat16.
+ *  - Return 0 on success or a negative status (-1 invalid argument, -2 unsupported shape/dtype,
+ *    -3 launch failure); dllm_last_error() then holds a message (thread-local).
+ *  - No entry point allocates device memory; outputs and intermediates are caller buffers.
+ *
+ * Citations name the reference (kotoba-lang/dllm-qwen38) interface each entry point replaces;
+ * [hf] = transformers/models/qwen3_5/modeling_qwen3_5.py (5.15.0).
+ */
+#ifndef DLLM_HIP_H
+#define DLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header/library pair. */
+int dllm_abi_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* dllm_last_error(void);
+
+/*
+ * Chunked gated delta rule with per-chunk states.
+ * Replaces src/dllm_qwen38/gdn.py:48-123 chunk_gated_delta_rule_with_states (and the core
+ * dispatch gdn.py:147-163 _core). q/k [B,T,Hk,Dk], v [B,T,Hv,Dv] with arbitrary batch/token/head
+ * strides (last dim contiguous); Hk divides Hv and value head j reads key head j/(Hv/Hk), so
+ * already-expanded q/k (Hk == Hv) are accepted as the reference passes them. g and beta
+ * [B,T,Hv] fp32 (the reference casts both to fp32, gdn.py:76-79). initial_state [B,Hv,Dk,Dv] fp32 or NULL (zeros).
+ * out [B,T,Hv,Dv] contiguous in the input dtype. states [B,T/chunk,Hv,Dk,Dv] fp32 (state after
+ * each chunk) or NULL for need_states=False. scale multiplies q after the optional l2norm
+ * (the reference uses Dk^-1/2). T % chunk != 0 fails with the reference's ValueError text.
+ * Dk, Dv <= 128.
+ */
+int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                       const void* v, const int64_t* v_strides, const float* g, const int64_t* g_strides,
+                       const float* beta, const int64_t* beta_strides, const float* initial_state,
+                       void* out, float* states, int B, int T, int Hk, int Hv, int Dk, int Dv,
+                       int chunk, int dtype, int use_qk_l2norm, float scale, void* stream);
+
+/*
+ * 1 if the fused state-fork kernel handles (Dk, block, dtype): block divides 32, Dk <= 128, and
+ * Dk <= 64 for float32. Otherwise callers run the two-pass fork (dllm_gdn_chunk_fwd on the clean
+ * stream with states, then again on the B*nb noised rows with initial states), as the reference
+ * does at src/dllm_qwen38/blockdiff.py:160-176.
+ */
+int dllm_gdn_fused_fork_supported(int Dk, int block, int dtype);
+
+/*
+ * Fused state fork of one GDN layer, both streams in one launch.
+ * Replaces the LINEAR arm of src/dllm_qwen38/blockdiff.py:153-177 (the clean pass
+ * gdn_mixer_forward(need_states=True) at :160, the state shift at :165-166 and the relaunch of
+ * every noised block as a batch row at :174-176), core part (gdn.py:221-231).
+ * qkv0/qkvt: post-conv activations [B,L,conv_dim] (strides in elements; channels contiguous)
+ * laid out as q | k | v channel blocks of Hk*Dk, Hk*Dk and Hv*Dv (gdn.py:221-224).
+ * beta* and g* [B,L,Hv] fp32, contiguous.
+ * out0/outt [B,L,Hv,Dv] contiguous: clean output, and noised output where noised block k of
+ * sequence b starts from the clean state after block k-1 (zeros for k = 0).
+ * states [B,L/block,Hv,Dk,Dv] fp32 (clean state after every block) or NULL.
+ */
+int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, int64_t qkv_stride_t,
+                            const float* beta0, const float* betat, const float* g0, const float* gt,
+                            void* out0, void* outt, float* states, int B, int L, int Hk, int Hv, int Dk,
+                            int Dv, int block, int dtype, float scale, void* stream);
+
+/*
+ * Causal depthwise conv + SiLU of both fork streams with conv-prefix carry-in.
+ * Replaces [hf]:219-239 causal_conv1d_fn as called at src/dllm_qwen38/gdn.py:217-219 for the clean
+ * stream and for the noised rows with the prefix cut at src/dllm_qwen38/blockdiff.py:167-173.
+ * raw0/rawt [B,L,conv_dim] token-major contiguous; weight [conv_dim,width] (+ optional bias).
+ * y0/yt [B,L,conv_dim] (input dtype). tails [B*nb,conv_dim,width-1] (input dtype) receives the
+ * clean pre-conv values before every block (zeros before the sequence start), or NULL.
+ * flags bit 0: the "no-conv-prefix" fault (noised blocks start cold, blockdiff.py:88,168-169).
+ * Computes in the weight dtype (fp32 accumulate, rounded to it), returns the input dtype.
+ */
+int dllm_conv_fork_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,
+                       void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
+                       int block, int dtype_x, int dtype_w, int flags, void* stream);
+
+/*
+ * Generic causal depthwise conv (+ optional SiLU) with an optional prefix.
+ * Replaces [hf]:219-239 causal_conv1d_fn on cat([conv_prefix, x]) keeping the last T outputs
+ * (src/dllm_qwen38/gdn.py:217-219). x [B,C,T] with strides {b,c,t}; prefix [B,C,prefix_len] with
+ * strides or NULL; weight [C,width], width <= 8. y is written token-major [B,T,C] contiguous.
+ */
+int dllm_causal_conv1d_fwd(const void* x, const int64_t* x_strides, const void* prefix,
+                           const int64_t* prefix_strides, int prefix_len, const void* weight,
+                           const void* bias, void* y, int B, int C, int T, int width, int dtype_x,
+                           int dtype_w, int activation, void* stream);
+
+/*
+ * Integer fork layout, computed on the device with the same index functions the kernels use.
+ * Replaces the index arithmetic of src/dllm_qwen38/blockdiff.py:161-173:
+ *   row[b*nb+k]          = fork batch row of (sequence b, block k)            (int32 [B*nb])
+ *   state_src[row]       = flat clean-state index b*nb+k-1 the row starts from, -1 = zeros
+ *   prefix_pos[row*(width-1)+j] = clean position feeding conv-prefix slot j, -1 = zero pad
+ */
+int dllm_fork_layout(int B, int L, int block, int width, int32_t* row, int32_t* state_src,
+                     int32_t* prefix_pos, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DLLM_HIP_H */

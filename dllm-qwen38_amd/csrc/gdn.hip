@@ -47,8 +47,8 @@ struct GdnArgs {
   int snap_every;  // tiles per chunk
   float scale;     // applied to q after l2norm
   int l2norm;
-  int vec_qk;      // 16-byte vector loads allowed for q/k rows
-  int vec_v;       // 16-byte vector loads allowed for v rows
+  int vec_qk;      // q/k rows: 16-byte vector loads (aligned, Dk equal to the kernel width)
+  int vec_v;       // v rows: 16-byte vector loads (aligned, Dv a multiple of 64)
 };
 
 // Linear workgroup id such that consecutive ids run on the same XCD (dispatch is round-robin over
@@ -79,33 +79,26 @@ struct GdnSmem {
   static constexpr int O_VEC = O_YF + 16 * 17 * 4;  // gam, bet, eg, egl (32 floats each)
   static constexpr int STREAM_BYTES = ((O_VEC + 4 * 32 * 4) + 15) & ~15;
   static constexpr int FRAG_BYTES = 16 * (int)sizeof(OpT);
-  static constexpr int O_SB = NS * STREAM_BYTES;  // fork: [2 buf][2 slice][KT][64 lanes] fragments
-  static constexpr int SB_BYTES = FORK ? 2 * 2 * KT * 64 * FRAG_BYTES : 0;
+  // state operand fragments published by the clean waves: [buffers][2 slices][KT][64 lanes]
+  // (double-buffered in fork mode, where the noised waves read them one tile later)
+  static constexpr int O_SB = NS * STREAM_BYTES;
+  static constexpr int SB_BYTES = (FORK ? 2 : 1) * 2 * KT * 64 * FRAG_BYTES;
   static constexpr int TOTAL = O_SB + SB_BYTES;
 };
 
-template <typename OpT, int N>
-__device__ __forceinline__ void load_row(const OpT* src, bool vec, int valid, float* dst) {
-  // N contiguous elements; `valid` of them are in range (rest zero)
-  if (vec && valid >= N) {
-    if constexpr (sizeof(OpT) == 2) {
+// N contiguous elements of a row into 16-byte vector registers (raw input dtype). `valid` of them are
+// in range, the rest are zero. Vector loads only when the whole run is in range and aligned.
+template <typename V, typename OpT, int N>
+__device__ __forceinline__ void load_raw(V* dst, const OpT* src, bool vec, int valid) {
+  constexpr int EPV = 16 / (int)sizeof(OpT);
+  if (vec) {  // uniform: every lane's run is in range (callers clamp rows), no divergence
 #pragma unroll
-      for (int i = 0; i < N; i += 8) {
-        const bf16x8 x = *(const bf16x8*)(src + i);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dst[i + e] = (float)x[e];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < N; i += 4) {
-        const f32x4 x = *(const f32x4*)(src + i);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[i + e] = x[e];
-      }
-    }
+    for (int i = 0; i < N / EPV; ++i) dst[i] = *(const V*)(src + i * EPV);
   } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) dst[i] = (i < valid) ? to_f32(src[i]) : 0.f;
+    for (int i = 0; i < N / EPV; ++i)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) dst[i][e] = (i * EPV + e < valid) ? src[i * EPV + e] : from_f32<OpT>(0.f);
   }
 }
 
@@ -121,7 +114,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform values live in SGPRs
+  const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
 
   const int nsl = (a.Dv + 63) >> 6;
   const int lin = xcd_linear_id(blockIdx.x, gridDim.x);
@@ -158,7 +152,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
   const bool col_ok = mycol < a.Dv;
 
   f32x16 S[KT];
-  F Sb[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) S[t] = zero16();
   if (role == 0) {
@@ -173,31 +166,61 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
         }
     }
 #pragma unroll
-    for (int t = 0; t < KT; ++t) acc_to_frag(S[t], Sb[t]);
-    if constexpr (FORK) {
-#pragma unroll
-      for (int t = 0; t < KT; ++t) *SBUF(0, my_sl, t) = Sb[t];
+    for (int t = 0; t < KT; ++t) {
+      F f;
+      acc_to_frag(S[t], f);
+      *SBUF(0, my_sl, t) = f;
     }
   }
+
+  // Raw inputs of one tile, held in registers so that the next tile's global loads are in flight
+  // while the current tile computes: thread -> (row lr, 1/8 of the q/k row, 8 v columns).
+  constexpr int NE = DK / 8;
+  constexpr int EPV = 16 / (int)sizeof(OpT);
+  using V16 = typename std::conditional<BF16, bf16x8, f32x4>::type;
+  V16 rq[NS][NE / EPV], rk[NS][NE / EPV], rv[NS][8 / EPV];
+  float rg[NS], rb[NS];
+  const int lr = tid >> 3, lseg = tid & 7;
+  const bool lreal = lr < a.sub;  // rows >= sub are zero padding (loaded from row 0, zeroed on use)
+  auto issue_loads = [&](int t0) {
+    const bool real = lreal;
+    const long long tok = t0 + (real ? lr : 0);
+    const int e0 = lseg * NE;
+    const int valid_qk = real ? max(0, min(NE, a.Dk - e0)) : 0;
+    const int c8 = col0 + lseg * 8;
+    const int valid_v = real ? max(0, min(8, a.Dv - c8)) : 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const GdnStream& st = a.s[s];
+      load_raw<V16, OpT, NE>(rq[s], (const OpT*)st.q + b * st.q_sb + tok * st.q_st + hk * st.q_sh + e0, a.vec_qk,
+                             valid_qk);
+      load_raw<V16, OpT, NE>(rk[s], (const OpT*)st.k + b * st.k_sb + tok * st.k_st + hk * st.k_sh + e0, a.vec_qk,
+                             valid_qk);
+      load_raw<V16, OpT, 8>(rv[s], (const OpT*)st.v + b * st.v_sb + tok * st.v_st + hv * st.v_sh + c8, a.vec_v,
+                            valid_v);
+      rg[s] = 0.f;
+      rb[s] = 0.f;
+      if (wave == 0 && h == 0 && l32 < a.sub) {
+        const long long tk = t0 + l32;
+        rg[s] = st.g[b * st.g_sb + tk * st.g_st + hv * st.g_sh];
+        rb[s] = st.beta[b * st.b_sb + tk * st.b_st + hv * st.b_sh];
+      }
+    }
+  };
+  issue_loads(0);
 
   for (int c = 0; c < ntiles; ++c) {
     const int t0 = c * a.sub;
     __syncthreads();  // previous tile's state phase is done with every LDS operand
 
-    // ------------------------------------------------------------------ load phase
+    // ------------------------------------------------------------------ load phase (registers -> LDS)
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const GdnStream& st = a.s[s];
-      // q and k rows: thread -> (row r, 1/8 of the row)
       {
-        constexpr int NE = DK / 8;
-        const int r = tid >> 3, seg = tid & 7, e0 = seg * NE;
-        const bool real = r < a.sub;
-        const int valid = real ? max(0, min(NE, a.Dk - e0)) : 0;
-        const long long tok = t0 + r;
+        const int e0 = lseg * NE;
         float x[NE];
-        // q
-        load_row<OpT, NE>((const OpT*)st.q + b * st.q_sb + tok * st.q_st + hk * st.q_sh + e0, a.vec_qk, valid, x);
+#pragma unroll
+        for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rq[s][i / EPV][i % EPV]) : 0.f;
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
@@ -205,11 +228,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
         ss += __shfl_xor(ss, 2);
         ss += __shfl_xor(ss, 4);
         float rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-        OpT* qh = QH(s) + r * QROW + e0;
+        OpT* qh = QH(s) + lr * QROW + e0;
 #pragma unroll
         for (int i = 0; i < NE; ++i) qh[i] = from_f32<OpT>((x[i] * rn) * a.scale);
-        // k
-        load_row<OpT, NE>((const OpT*)st.k + b * st.k_sb + tok * st.k_st + hk * st.k_sh + e0, a.vec_qk, valid, x);
+#pragma unroll
+        for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rk[s][i / EPV][i % EPV]) : 0.f;
         ss = 0.f;
 #pragma unroll
         for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
@@ -217,52 +240,37 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
         ss += __shfl_xor(ss, 2);
         ss += __shfl_xor(ss, 4);
         rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-        OpT* kh = KH(s) + r * QROW + e0;
-        OpT* kt = KTr(s) + e0 * TROW + r;
+        OpT* kh = KH(s) + lr * QROW + e0;
+        OpT* kt = KTr(s) + e0 * TROW + lr;
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
           const OpT y = from_f32<OpT>(x[i] * rn);
           kh[i] = y;
           kt[i * TROW] = y;
         }
-      }
-      // v rows of this workgroup's 64 columns: thread -> (row r, 8 columns)
-      {
-        const int r = tid >> 3, seg = tid & 7, c8 = col0 + seg * 8;
-        const bool real = r < a.sub;
-        const int valid = real ? max(0, min(8, a.Dv - c8)) : 0;
-        float x[8];
-        load_row<OpT, 8>((const OpT*)st.v + b * st.v_sb + (long long)(t0 + r) * st.v_st + hv * st.v_sh + c8,
-                         a.vec_v, valid, x);
-        OpT* vt = VT(s) + (seg * 8) * TROW + r;
+        OpT* vt = VT(s) + (lseg * 8) * TROW + lr;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vt[i * TROW] = from_f32<OpT>(x[i]);
+        for (int i = 0; i < 8; ++i) vt[i * TROW] = lreal ? rv[s][i / EPV][i % EPV] : from_f32<OpT>(0.f);
       }
       // beta, g and the cumulative decay (sequential order, as a cumsum)
       if (wave == 0) {
         const int r = l32;
-        const bool real = r < a.sub;
-        const long long tok = t0 + r;
-        float gv = 0.f, bt = 0.f;
-        if (real && h == 0) {
-          gv = st.g[b * st.g_sb + tok * st.g_st + hv * st.g_sh];
-          bt = st.beta[b * st.b_sb + tok * st.b_st + hv * st.b_sh];
-        }
         float gam = 0.f;
         for (int q = 0; q < 32; ++q) {
-          const float gq = __shfl(gv, q, 64);
+          const float gq = __shfl(rg[s], q, 64);
           if (q <= r) gam += gq;
         }
         const float glast = __shfl(gam, 31, 64);
         if (h == 0) {
           GAM(s)[r] = gam;
-          BET(s)[r] = bt;
+          BET(s)[r] = rb[s];
           EG(s)[r] = expf(gam);
           EGL(s)[r] = expf(glast - gam);
         }
       }
     }
     __syncthreads();
+    if (c + 1 < ntiles) issue_loads(t0 + a.sub);  // next tile's inputs travel during this tile
 
     // ------------------------------------------------------------------ G (+ T) phase
     {
@@ -420,14 +428,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
     // ------------------------------------------------------------------ state phase
     if (role == 0 || FORK) {
       const int s = role;  // stream
-      F Sx[KT];
-      if (role == 0) {
-#pragma unroll
-        for (int t = 0; t < KT; ++t) Sx[t] = Sb[t];
-      } else {
-#pragma unroll
-        for (int t = 0; t < KT; ++t) Sx[t] = *SBUF(c & 1, my_sl, t);
-      }
+      const int sbuf = FORK ? (c & 1) : 0;
       f32x16 accU = zero16(), accWS = zero16(), accQS = zero16();
       {
         F fa, fb;
@@ -440,8 +441,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
         F fw, fq;
         lds_frag(KH(s) + l32 * QROW + kt * 32, h, fw);
         lds_frag(QH(s) + l32 * QROW + kt * 32, h, fq);
-        mma32(accWS, fw, Sx[kt]);
-        mma32(accQS, fq, Sx[kt]);
+        const F sx = *SBUF(sbuf, my_sl, kt);
+        mma32(accWS, fw, sx);
+        mma32(accQS, fq, sx);
       }
       const float* eg = EG(s);
       f32x16 vn;
@@ -459,11 +461,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
       }
       // output rows of the real tokens
       if (col_ok) {
-        OpT* out = (OpT*)a.s[s].out;
+        const long long rs = (long long)a.Hv * a.Dv;  // token stride of out
+        OpT* ob = (OpT*)a.s[s].out + ((long long)b * a.T + t0) * rs + (long long)hv * a.Dv + col0 + my_sl * 32;
+        const unsigned lo = (unsigned)(4 * h) * (unsigned)rs + (unsigned)l32;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int i = rho(v, h);
-          if (i < a.sub) out[(((long long)b * a.T + t0 + i) * a.Hv + hv) * a.Dv + mycol] = from_f32<OpT>(accQS[v]);
+          const int ru = ((v >> 2) << 3) + (v & 3);  // row = ru + 4h
+          if (ru + 4 * h < a.sub) (ob + ru * rs)[lo] = from_f32<OpT>(accQS[v]);
         }
       }
       if (role == 0) {
@@ -484,20 +488,21 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
         }
         if (a.states && ((c + 1) % a.snap_every) == 0 && col_ok) {
           const int sn = (c + 1) / a.snap_every - 1;
-          float* dst = a.states + (((long long)b * nsnap + sn) * a.Hv + hv) * (long long)a.Dk * a.Dv + mycol;
+          float* sb = a.states + (((long long)b * nsnap + sn) * a.Hv + hv) * (long long)a.Dk * a.Dv + col0 + my_sl * 32;
+          const unsigned lo = (unsigned)(4 * h * a.Dv + l32);
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-              const int dk = 32 * kt + rho(v, h);
-              if (dk < a.Dk) __builtin_nontemporal_store(S[kt][v], dst + (long long)dk * a.Dv);
+              const int du = 32 * kt + ((v >> 2) << 3) + (v & 3);  // dk = du + 4h
+              if (du + 4 * h < a.Dk) __builtin_nontemporal_store(S[kt][v], (sb + (long long)du * a.Dv) + lo);
             }
         }
 #pragma unroll
-        for (int t = 0; t < KT; ++t) acc_to_frag(S[t], Sb[t]);
-        if constexpr (FORK) {
-#pragma unroll
-          for (int t = 0; t < KT; ++t) *SBUF((c + 1) & 1, my_sl, t) = Sb[t];
+        for (int t = 0; t < KT; ++t) {
+          F f;
+          acc_to_frag(S[t], f);
+          *SBUF(FORK ? ((c + 1) & 1) : 0, my_sl, t) = f;
         }
       }
     }
@@ -577,8 +582,9 @@ extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const
   const int esz = dtype == DT_BF16 ? 2 : 4;
   const int vel = 16 / esz;
   auto st_ok = [&](const int64_t* st3) { return (st3[0] % vel == 0) && (st3[1] % vel == 0) && (st3[2] % vel == 0); };
-  a.vec_qk = aligned16(q) && aligned16(k) && st_ok(q_strides) && st_ok(k_strides);
-  a.vec_v = aligned16(v) && st_ok(v_strides);
+  const int dkw = Dk <= 64 ? 64 : 128;
+  a.vec_qk = aligned16(q) && aligned16(k) && st_ok(q_strides) && st_ok(k_strides) && Dk == dkw;
+  a.vec_v = aligned16(v) && st_ok(v_strides) && (Dv % 64 == 0);
   return dispatch_gdn(a, dtype, false, (hipStream_t)stream);
 }
 
@@ -622,7 +628,8 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
   const int vel = 16 / esz;
   const bool st_ok = (qkv_stride_b % vel == 0) && (qkv_stride_t % vel == 0) && (Dk % vel == 0) && (Dv % vel == 0) &&
                      ((long long)Hk * Dk % vel == 0);
-  a.vec_qk = aligned16(qkv0) && aligned16(qkvt) && st_ok;
-  a.vec_v = a.vec_qk;
+  const int dkw = Dk <= 64 ? 64 : 128;
+  a.vec_qk = aligned16(qkv0) && aligned16(qkvt) && st_ok && Dk == dkw;
+  a.vec_v = aligned16(qkv0) && aligned16(qkvt) && st_ok && (Dv % 64 == 0);
   return dispatch_gdn(a, dtype, true, (hipStream_t)stream);
 }

@@ -1,23 +1,26 @@
 // Chunked gated delta rule with per-chunk states and the fused state fork (gfx950 / CDNA4).
 //
-// One workgroup (4 wavefronts) owns one (sequence b, value head hv, 64-column Dv window) and walks
-// the sequence in 32-row tiles. A tile holds `sub` real tokens (sub = gcd(chunk, 32)); the rest
-// are zero rows, which are exact no-ops of the recurrence (k = q = v = 0, beta = 0, g = 0).
+// One workgroup owns one (sequence b, value head hv, window of DVW value columns) and walks the
+// sequence in 32-row tiles. A tile holds `sub` real tokens (sub = gcd(chunk, 32)); the other rows
+// are zero, which are exact no-ops of the recurrence (k = q = v = 0, beta = 0, g = 0).
 //
-// Per tile, for each stream (clean; plus noised in fork mode):
-//   load    q, k (key head hv / (Hv/Hk): GQA by indexing, no expansion), v, beta, g;
-//           l2norm + Dk^-1/2 in fp32; gamma = sequential cumsum of g; operands into LDS.
+// Waves: a set of 4 wavefronts per stream (clean; plus noised in fork mode, 8 waves in total, so
+// every SIMD runs one clean and one noised wave and each hides the other's latency).
+// Per tile and stream:
+//   load    q, k (key head hv / (Hv/Hk): GQA by indexing, no expansion), v, beta, g from the
+//           registers prefetched during the previous tile; l2norm (DPP reductions) and Dk^-1/2 in
+//           fp32; gamma = sequential cumsum of g; operands into LDS.
 //   G       K^K^T and Q^K^T on MFMA; decay/beta masks -> A (fp32), P.
 //   T       T = (I + A)^-1 in fp32 by a blocked inverse (8x8 diagonal blocks by forward
-//           substitution, then 8x8 and 16x16 off-diagonal blocks by products), entirely inside the
-//           wavefront that produced A; T1 = T diag(beta e^gamma), T2 = T diag(beta).
+//           substitution, then 8x8 and 16x16 off-diagonal blocks by products) inside the wave
+//           that produced A; T1 = T diag(beta e^gamma), T2 = T diag(beta).
 //   W       W = T1 K^ (= (I+A)^-1 (beta K^ e^gamma)) on MFMA, written over K^.
-//   state   clean wave: U = T2 V, V' = U - W S, O = e^gamma (Q^ S) + P V',
+//   state   wave u of the clean set: U = T2 V, V' = U - W S, O = e^gamma (Q^ S) + P V',
 //           S <- e^gamma_last S + K^T (e^(gamma_last - gamma) V'), snapshot S every chunk;
-//           noised wave (fork): the same O with the noised tile's operands and the clean state
-//           before the tile, which the clean wave publishes through LDS.
-// The recurrent state S (Dk x 32 columns per wave) lives in fp32 MFMA accumulators for the whole
-// sequence and is fed back as the B operand directly from the accumulator layout (rho order).
+//           wave u of the noised set: the same O with the noised tile's operands and the clean
+//           state before the tile, published by the clean set through LDS.
+// The recurrent state S (Dk x 32 columns per clean wave) lives in fp32 MFMA accumulators for the
+// whole sequence and is fed back as the B operand directly from the accumulator layout.
 #include <type_traits>
 
 #include "common.h"
@@ -30,25 +33,22 @@ struct GdnStream {
   const void* v;
   const float* beta;
   const float* g;
-  void* out;
-  long long q_sb, q_st, q_sh;
-  long long k_sb, k_st, k_sh;
-  long long v_sb, v_st, v_sh;
-  long long b_sb, b_st, b_sh;
-  long long g_sb, g_st, g_sh;
+  void* out;  // [B, T, Hv, Dv] contiguous
 };
 
 struct GdnArgs {
   GdnStream s[2];
   const float* init;  // [B, Hv, Dk, Dv] fp32 or null
   float* states;      // [B, T/chunk, Hv, Dk, Dv] fp32 or null
+  long long q_sb, k_sb, v_sb, b_sb, g_sb;  // batch strides (elements)
+  int q_st, q_sh, k_st, k_sh, v_st, v_sh, b_st, b_sh, g_st, g_sh;  // token / head strides
   int B, T, Hk, Hv, Dk, Dv;
   int sub;         // real rows per 32-row tile
   int snap_every;  // tiles per chunk
   float scale;     // applied to q after l2norm
   int l2norm;
-  int vec_qk;      // q/k rows: 16-byte vector loads (aligned, Dk equal to the kernel width)
-  int vec_v;       // v rows: 16-byte vector loads (aligned, Dv a multiple of 64)
+  int vec_qk;  // q/k rows: 16-byte vector loads (aligned, Dk equal to the kernel width)
+  int vec_v;   // v rows: 16-byte vector loads (aligned, Dv a multiple of the column window)
 };
 
 // Linear workgroup id such that consecutive ids run on the same XCD (dispatch is round-robin over
@@ -58,19 +58,35 @@ __device__ __forceinline__ int xcd_linear_id(int bid, int n) {
   return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
 }
 
-template <int DK, bool BF16, bool FORK>
+// Returns x unchanged but opaque to the optimiser, so that uniform addresses derived from it are
+// computed where they are used instead of being hoisted out of the tile loop (and spilled).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
+// Sum over each aligned group of 8 lanes, returned to all 8 (DPP: no LDS round trip). The three
+// steps are quad_perm [1,0,3,2], quad_perm [2,3,0,1] and row_half_mirror.
+__device__ __forceinline__ float dpp_sum8(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
+  return x;
+}
+
+template <int DK, int DVW, bool BF16, bool FORK>
 struct GdnSmem {
   using OpT = typename std::conditional<BF16, bf16, float>::type;
   static constexpr int NS = FORK ? 2 : 1;
   static constexpr int KT = DK / 32;
+  static constexpr int NSL = DVW / 32;
   static constexpr int QROW = DK + (BF16 ? 8 : 4);  // [32][DK] row stride (elements)
-  static constexpr int TROW = 32 + (BF16 ? 8 : 4);  // [.][32] row stride (elements)
-  // per-stream byte offsets
+  static constexpr int TROW = 36;                    // [.][32] row stride (elements)
   static constexpr int O_QH = 0;
   static constexpr int O_KH = O_QH + 32 * QROW * (int)sizeof(OpT);
   static constexpr int O_KT = O_KH + 32 * QROW * (int)sizeof(OpT);
   static constexpr int O_VT = O_KT + DK * TROW * (int)sizeof(OpT);
-  static constexpr int O_P = O_VT + 64 * TROW * (int)sizeof(OpT);
+  static constexpr int O_P = O_VT + DVW * TROW * (int)sizeof(OpT);
   static constexpr int O_T1 = O_P + 32 * TROW * (int)sizeof(OpT);
   static constexpr int O_T2 = O_T1 + 32 * TROW * (int)sizeof(OpT);
   static constexpr int O_AF = O_T2 + 32 * TROW * (int)sizeof(OpT);
@@ -79,36 +95,56 @@ struct GdnSmem {
   static constexpr int O_VEC = O_YF + 16 * 17 * 4;  // gam, bet, eg, egl (32 floats each)
   static constexpr int STREAM_BYTES = ((O_VEC + 4 * 32 * 4) + 15) & ~15;
   static constexpr int FRAG_BYTES = 16 * (int)sizeof(OpT);
-  // state operand fragments published by the clean waves: [buffers][2 slices][KT][64 lanes]
-  // (double-buffered in fork mode, where the noised waves read them one tile later)
+  // state operand fragments published by the clean set for the noised set: [NSL][KT][64 lanes]
   static constexpr int O_SB = NS * STREAM_BYTES;
-  static constexpr int SB_BYTES = (FORK ? 2 : 1) * 2 * KT * 64 * FRAG_BYTES;
+  static constexpr int SB_BYTES = FORK ? NSL * KT * 64 * FRAG_BYTES : 0;
   static constexpr int TOTAL = O_SB + SB_BYTES;
 };
 
-// N contiguous elements of a row into 16-byte vector registers (raw input dtype). `valid` of them are
-// in range, the rest are zero. Vector loads only when the whole run is in range and aligned.
+// Two runs of N/2 elements of a row into 16-byte vector registers of the raw input dtype.
+// `valid0/1` elements of each run are in range, the rest are zero. When a run is shorter than one
+// vector the two runs are contiguous (src1 == src0 + N/2) and load as one vector.
 template <typename V, typename OpT, int N>
-__device__ __forceinline__ void load_raw(V* dst, const OpT* src, bool vec, int valid) {
+__device__ __forceinline__ void load_runs(V* dst, const OpT* src0, const OpT* src1, bool vec, int valid0,
+                                          int valid1) {
   constexpr int EPV = 16 / (int)sizeof(OpT);
-  if (vec) {  // uniform: every lane's run is in range (callers clamp rows), no divergence
+  constexpr int H = N / 2;
+  if constexpr (H >= EPV) {
+    constexpr int NV = H / EPV;  // vectors per run
+    if (vec) {  // uniform: every lane's runs are in range (callers clamp rows), no divergence
 #pragma unroll
-    for (int i = 0; i < N / EPV; ++i) dst[i] = *(const V*)(src + i * EPV);
+      for (int i = 0; i < NV; ++i) {
+        dst[i] = *(const V*)(src0 + i * EPV);
+        dst[NV + i] = *(const V*)(src1 + i * EPV);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          dst[i][e] = (i * EPV + e < valid0) ? src0[i * EPV + e] : from_f32<OpT>(0.f);
+          dst[NV + i][e] = (i * EPV + e < valid1) ? src1[i * EPV + e] : from_f32<OpT>(0.f);
+        }
+    }
   } else {
+    static_assert(N == EPV, "a short row segment must be exactly one vector");
+    if (vec) {
+      dst[0] = *(const V*)src0;
+    } else {
 #pragma unroll
-    for (int i = 0; i < N / EPV; ++i)
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) dst[i][e] = (i * EPV + e < valid) ? src[i * EPV + e] : from_f32<OpT>(0.f);
+      for (int e = 0; e < N; ++e)
+        dst[0][e] = ((e < H) ? (e < valid0) : (e - H < valid1)) ? src0[e] : from_f32<OpT>(0.f);
+    }
   }
 }
 
-template <int DK, bool BF16, bool FORK>
-__global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
-  using SM = GdnSmem<DK, BF16, FORK>;
+template <int DK, int DVW, bool BF16, bool FORK>
+__global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) {
+  using SM = GdnSmem<DK, DVW, BF16, FORK>;
   using OpT = typename SM::OpT;
   using F = Frag<BF16>;
-  constexpr int NS = SM::NS;
   constexpr int KT = SM::KT;
+  constexpr int NSL = SM::NSL;
   constexpr int QROW = SM::QROW;
   constexpr int TROW = SM::TROW;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
@@ -116,156 +152,176 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform values live in SGPRs
   const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int set = FORK ? (wave >> 2) : 0;  // stream of this wave's set
+  const int u = wave & 3;                  // wave within the set
+  const int ts = tid & 255;                // thread within the set
 
-  const int nsl = (a.Dv + 63) >> 6;
+  const int nwin = (a.Dv + DVW - 1) / DVW;
   const int lin = xcd_linear_id(blockIdx.x, gridDim.x);
-  const int slice = lin % nsl;
-  const int hv = (lin / nsl) % a.Hv;
-  const int b = lin / (nsl * a.Hv);
+  const int win = lin % nwin;
+  const int hv = (lin / nwin) % a.Hv;
+  const int b = lin / (nwin * a.Hv);
   const int hk = hv / (a.Hv / a.Hk);
-  const int col0 = slice * 64;
+  const int col0 = win * DVW;
   const int ntiles = a.T / a.sub;
   const int nsnap = a.T / (a.sub * a.snap_every);
 
-  auto QH = [&](int s) { return (OpT*)(smem + s * SM::STREAM_BYTES + SM::O_QH); };
-  auto KH = [&](int s) { return (OpT*)(smem + s * SM::STREAM_BYTES + SM::O_KH); };
-  auto KTr = [&](int s) { return (OpT*)(smem + s * SM::STREAM_BYTES + SM::O_KT); };
-  auto VT = [&](int s) { return (OpT*)(smem + s * SM::STREAM_BYTES + SM::O_VT); };
-  auto PP = [&](int s) { return (OpT*)(smem + s * SM::STREAM_BYTES + SM::O_P); };
-  auto T1 = [&](int s) { return (OpT*)(smem + s * SM::STREAM_BYTES + SM::O_T1); };
-  auto T2 = [&](int s) { return (OpT*)(smem + s * SM::STREAM_BYTES + SM::O_T2); };
-  auto AF = [&](int s) { return (float*)(smem + s * SM::STREAM_BYTES + SM::O_AF); };
-  auto TF = [&](int s) { return (float*)(smem + s * SM::STREAM_BYTES + SM::O_TF); };
-  auto YF = [&](int s) { return (float*)(smem + s * SM::STREAM_BYTES + SM::O_YF); };
-  auto GAM = [&](int s) { return (float*)(smem + s * SM::STREAM_BYTES + SM::O_VEC); };
-  auto BET = [&](int s) { return GAM(s) + 32; };
-  auto EG = [&](int s) { return GAM(s) + 64; };
-  auto EGL = [&](int s) { return GAM(s) + 96; };
-  auto SBUF = [&](int buf, int sl, int kt) {
-    return (F*)(smem + SM::O_SB) + (((buf * 2 + sl) * KT + kt) * 64 + lane);
-  };
+  unsigned char* sbase = smem + set * SM::STREAM_BYTES;
+  OpT* const QH = (OpT*)(sbase + SM::O_QH);
+  OpT* const KH = (OpT*)(sbase + SM::O_KH);
+  OpT* const KTr = (OpT*)(sbase + SM::O_KT);
+  OpT* const VT = (OpT*)(sbase + SM::O_VT);
+  OpT* const PP = (OpT*)(sbase + SM::O_P);
+  OpT* const T1 = (OpT*)(sbase + SM::O_T1);
+  OpT* const T2 = (OpT*)(sbase + SM::O_T2);
+  float* const AF = (float*)(sbase + SM::O_AF);
+  float* const TF = (float*)(sbase + SM::O_TF);
+  float* const YF = (float*)(sbase + SM::O_YF);
+  float* const GAM = (float*)(sbase + SM::O_VEC);
+  float* const BET = GAM + 32;
+  float* const EG = GAM + 64;
+  float* const EGL = GAM + 96;
+  auto SBUF = [&](int sl, int kt) { return (F*)(smem + SM::O_SB) + ((sl * KT + kt) * 64 + lane); };
 
-  // state-phase roles: wave -> (32-column slice, stream)
-  const int my_sl = wave & 1;
-  const int role = wave >> 1;  // 0 clean (owns S); 1 noised (fork) or idle
-  const int mycol = col0 + my_sl * 32 + l32;
-  const bool col_ok = mycol < a.Dv;
+  // this set's stream: base pointers at (b, head)
+  const GdnStream& st = a.s[set];
+  const OpT* const qb = (const OpT*)st.q + b * a.q_sb + (long long)hk * a.q_sh;
+  const OpT* const kb = (const OpT*)st.k + b * a.k_sb + (long long)hk * a.k_sh;
+  const OpT* const vb = (const OpT*)st.v + b * a.v_sb + (long long)hv * a.v_sh;
+  const float* const betab = st.beta + b * a.b_sb + (long long)hv * a.b_sh;
+  const float* const gb = st.g + b * a.g_sb + (long long)hv * a.g_sh;
+
+  // state-phase role: wave u of the set owns value columns [col0 + 32u, col0 + 32u + 32)
+  const bool state_wave = u < NSL;
+  const int scol0 = col0 + u * 32;  // wave-uniform
+  const bool slice_full = scol0 + 32 <= a.Dv;
+  const bool col_ok = scol0 + l32 < a.Dv;
 
   f32x16 S[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) S[t] = zero16();
-  if (role == 0) {
-    if (a.init && col_ok) {
-      const float* src = a.init + ((long long)(b * a.Hv + hv) * a.Dk) * a.Dv + mycol;
+  if (set == 0 && state_wave && a.init && col_ok) {
+    const float* src = a.init + ((long long)(b * a.Hv + hv) * a.Dk) * a.Dv + scol0 + l32;
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
+    for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int dk = 32 * t + rho(v, h);
-          if (dk < a.Dk) S[t][v] = src[(long long)dk * a.Dv];
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < KT; ++t) {
-      F f;
-      acc_to_frag(S[t], f);
-      *SBUF(0, my_sl, t) = f;
-    }
+      for (int v = 0; v < 16; ++v) {
+        const int dk = 32 * t + rho(v, h);
+        if (dk < a.Dk) S[t][v] = src[(long long)dk * a.Dv];
+      }
   }
 
-  // Raw inputs of one tile, held in registers so that the next tile's global loads are in flight
-  // while the current tile computes: thread -> (row lr, 1/8 of the q/k row, 8 v columns).
-  constexpr int NE = DK / 8;
+  // Raw inputs of one tile, in registers so that the next tile's global loads travel while the
+  // current tile computes. Thread (row lr, segment lseg) holds two runs of its row: q/k columns
+  // [NE/2*lseg, +NE/2) and [DK/2 + NE/2*lseg, +NE/2), v columns likewise in the DVW window (two
+  // runs per thread keep the transposed LDS writes nearly conflict-free).
+  constexpr int NE = DK / 8;   // q/k elements per thread
+  constexpr int NV = DVW / 8;  // v elements per thread
   constexpr int EPV = 16 / (int)sizeof(OpT);
   using V16 = typename std::conditional<BF16, bf16x8, f32x4>::type;
-  V16 rq[NS][NE / EPV], rk[NS][NE / EPV], rv[NS][8 / EPV];
-  float rg[NS], rb[NS];
-  const int lr = tid >> 3, lseg = tid & 7;
+  V16 rq[NE / EPV], rk[NE / EPV], rv[NV / EPV];
+  float rg = 0.f, rb = 0.f;
+  const int lr = ts >> 3, lseg = ts & 7;
   const bool lreal = lr < a.sub;  // rows >= sub are zero padding (loaded from row 0, zeroed on use)
+  constexpr bool TWO_QK = (NE / 2) >= EPV;  // else one contiguous run of NE elements
+  constexpr bool TWO_V = (NV / 2) >= EPV;
+  const int qe0 = TWO_QK ? lseg * (NE / 2) : lseg * NE;
+  const int qe1 = TWO_QK ? DK / 2 + lseg * (NE / 2) : qe0 + NE / 2;
+  const int ve0 = TWO_V ? lseg * (NV / 2) : lseg * NV;
+  const int ve1 = TWO_V ? DVW / 2 + lseg * (NV / 2) : ve0 + NV / 2;
   auto issue_loads = [&](int t0) {
-    const bool real = lreal;
-    const long long tok = t0 + (real ? lr : 0);
-    const int e0 = lseg * NE;
-    const int valid_qk = real ? max(0, min(NE, a.Dk - e0)) : 0;
-    const int c8 = col0 + lseg * 8;
-    const int valid_v = real ? max(0, min(8, a.Dv - c8)) : 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const GdnStream& st = a.s[s];
-      load_raw<V16, OpT, NE>(rq[s], (const OpT*)st.q + b * st.q_sb + tok * st.q_st + hk * st.q_sh + e0, a.vec_qk,
-                             valid_qk);
-      load_raw<V16, OpT, NE>(rk[s], (const OpT*)st.k + b * st.k_sb + tok * st.k_st + hk * st.k_sh + e0, a.vec_qk,
-                             valid_qk);
-      load_raw<V16, OpT, 8>(rv[s], (const OpT*)st.v + b * st.v_sb + tok * st.v_st + hv * st.v_sh + c8, a.vec_v,
-                            valid_v);
-      rg[s] = 0.f;
-      rb[s] = 0.f;
-      if (wave == 0 && h == 0 && l32 < a.sub) {
-        const long long tk = t0 + l32;
-        rg[s] = st.g[b * st.g_sb + tk * st.g_st + hv * st.g_sh];
-        rb[s] = st.beta[b * st.b_sb + tk * st.b_st + hv * st.b_sh];
-      }
+    const int tok = t0 + (lreal ? lr : 0);
+    const int vq0 = lreal ? max(0, min(NE / 2, a.Dk - qe0)) : 0;
+    const int vq1 = lreal ? max(0, min(NE / 2, a.Dk - qe1)) : 0;
+    const int vv0 = lreal ? max(0, min(NV / 2, a.Dv - col0 - ve0)) : 0;
+    const int vv1 = lreal ? max(0, min(NV / 2, a.Dv - col0 - ve1)) : 0;
+    const OpT* qr = qb + tok * a.q_st;
+    const OpT* kr = kb + tok * a.k_st;
+    const OpT* vr = vb + tok * a.v_st + col0;
+    load_runs<V16, OpT, NE>(rq, qr + qe0, qr + qe1, a.vec_qk, vq0, vq1);
+    load_runs<V16, OpT, NE>(rk, kr + qe0, kr + qe1, a.vec_qk, vq0, vq1);
+    load_runs<V16, OpT, NV>(rv, vr + ve0, vr + ve1, a.vec_v, vv0, vv1);
+    if (u == 0 && h == 0 && l32 < a.sub) {
+      rg = gb[(t0 + l32) * a.g_st];
+      rb = betab[(t0 + l32) * a.b_st];
+    } else {
+      rg = 0.f;
+      rb = 0.f;
     }
   };
   issue_loads(0);
 
   for (int c = 0; c < ntiles; ++c) {
     const int t0 = c * a.sub;
-    __syncthreads();  // previous tile's state phase is done with every LDS operand
+    __syncthreads();  // the previous tile's state phase is done with every LDS operand
 
     // ------------------------------------------------------------------ load phase (registers -> LDS)
+    {
+      float x[NE];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      {
-        const int e0 = lseg * NE;
-        float x[NE];
+      for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rq[i / EPV][i % EPV]) : 0.f;
+      float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rq[s][i / EPV][i % EPV]) : 0.f;
-        float ss = 0.f;
+      for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
+      ss = dpp_sum8(ss);
+      float rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
 #pragma unroll
-        for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 4);
-        float rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-        OpT* qh = QH(s) + lr * QROW + e0;
-#pragma unroll
-        for (int i = 0; i < NE; ++i) qh[i] = from_f32<OpT>((x[i] * rn) * a.scale);
-#pragma unroll
-        for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rk[s][i / EPV][i % EPV]) : 0.f;
-        ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 4);
-        rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-        OpT* kh = KH(s) + lr * QROW + e0;
-        OpT* kt = KTr(s) + e0 * TROW + lr;
-#pragma unroll
-        for (int i = 0; i < NE; ++i) {
-          const OpT y = from_f32<OpT>(x[i] * rn);
-          kh[i] = y;
-          kt[i * TROW] = y;
-        }
-        OpT* vt = VT(s) + (lseg * 8) * TROW + lr;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vt[i * TROW] = lreal ? rv[s][i / EPV][i % EPV] : from_f32<OpT>(0.f);
+      for (int i = 0; i < NE / 2; ++i) {
+        QH[lr * QROW + qe0 + i] = from_f32<OpT>((x[i] * rn) * a.scale);
+        QH[lr * QROW + qe1 + i] = from_f32<OpT>((x[NE / 2 + i] * rn) * a.scale);
       }
-      // beta, g and the cumulative decay (sequential order, as a cumsum)
-      if (wave == 0) {
-        const int r = l32;
-        float gam = 0.f;
-        for (int q = 0; q < 32; ++q) {
-          const float gq = __shfl(rg[s], q, 64);
-          if (q <= r) gam += gq;
+#pragma unroll
+      for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rk[i / EPV][i % EPV]) : 0.f;
+      ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
+      ss = dpp_sum8(ss);
+      rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
+#pragma unroll
+      for (int i = 0; i < NE / 2; ++i) {
+        const OpT y0 = from_f32<OpT>(x[i] * rn);
+        const OpT y1 = from_f32<OpT>(x[NE / 2 + i] * rn);
+        KH[lr * QROW + qe0 + i] = y0;
+        KH[lr * QROW + qe1 + i] = y1;
+        KTr[(qe0 + i) * TROW + lr] = y0;
+        KTr[(qe1 + i) * TROW + lr] = y1;
+      }
+#pragma unroll
+      for (int i = 0; i < NV / 2; ++i) {
+        VT[(ve0 + i) * TROW + lr] = lreal ? rv[i / EPV][i % EPV] : from_f32<OpT>(0.f);
+        VT[(ve1 + i) * TROW + lr] = lreal ? rv[(NV / 2 + i) / EPV][(NV / 2 + i) % EPV] : from_f32<OpT>(0.f);
+      }
+      // beta, g and the cumulative decay in sequential order (as a cumsum), one wave per set
+      if (u == 0) {
+        if (h == 0) GAM[l32] = rg;
+        wave_lds_sync();
+        float gam = 0.f, gall = 0.f;
+#pragma unroll
+        for (int q = 0; q < 32; q += 4) {
+          const f32x4 g4 = *(const f32x4*)(GAM + q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (q + e <= l32) gam += g4[e];
+            gall += g4[e];
+          }
         }
-        const float glast = __shfl(gam, 31, 64);
+        wave_lds_sync();
         if (h == 0) {
-          GAM(s)[r] = gam;
-          BET(s)[r] = rb[s];
-          EG(s)[r] = expf(gam);
-          EGL(s)[r] = expf(glast - gam);
+          GAM[l32] = gam;
+          BET[l32] = rb;
+          EG[l32] = expf(gam);
+          EGL[l32] = expf(gall - gam);
+        }
+      }
+      // the clean set publishes the state before this tile for the noised set
+      if constexpr (FORK) {
+        if (set == 0 && state_wave) {
+#pragma unroll
+          for (int t = 0; t < KT; ++t) {
+            F f;
+            acc_to_frag(S[t], f);
+            *SBUF(u, t) = f;
+          }
         }
       }
     }
@@ -274,46 +330,38 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
 
     // ------------------------------------------------------------------ G (+ T) phase
     {
-      const int gs = FORK ? (wave & 1) : 0;
-      const bool isG = FORK ? (wave < 2) : (wave == 0);
-      const bool isQK = FORK ? (wave >= 2) : (wave == 1);
+      // Gram + T on waves 0 / 5 and QK^T on waves 2 / 7: four different SIMDs in fork mode
+      const bool isG = (u == (set == 0 ? 0 : 1));
+      const bool isQK = (u == (set == 0 ? 2 : 3));
       if (isG || isQK) {
-        const OpT* X = isG ? KH(gs) : QH(gs);
-        const OpT* Kr = KH(gs);
+        const OpT* X = isG ? KH : QH;
         f32x16 acc = zero16();
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
           F fa, fb;
           lds_frag(X + l32 * QROW + kt * 32, h, fa);
-          lds_frag(Kr + l32 * QROW + kt * 32, h, fb);
+          lds_frag(KH + l32 * QROW + kt * 32, h, fb);
           mma32(acc, fa, fb);
         }
-        const float* gam = GAM(gs);
-        const float gj = gam[l32];
+        const float gj = GAM[l32];
         if (isG) {
-          const float* bet = BET(gs);
-          float* Af = AF(gs);
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int i = rho(v, h);
-            Af[i * 33 + l32] = (l32 < i) ? bet[i] * acc[v] * expf(gam[i] - gj) : 0.f;
+            AF[i * 33 + l32] = (l32 < i) ? BET[i] * acc[v] * expf(GAM[i] - gj) : 0.f;
           }
         } else {
-          OpT* P = PP(gs);
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int i = rho(v, h);
-            P[i * TROW + l32] = from_f32<OpT>((l32 <= i) ? acc[v] * expf(gam[i] - gj) : 0.f);
+            PP[i * TROW + l32] = from_f32<OpT>((l32 <= i) ? acc[v] * expf(GAM[i] - gj) : 0.f);
           }
         }
       }
       if (isG) {
         // T = (I + A)^-1, fp32, inside this wavefront
-        const float* Af = AF(gs);
-        float* Tf = TF(gs);
-        float* Yf = YF(gs);
 #pragma unroll
-        for (int m = 0; m < 16; ++m) Tf[(m * 2 + h) * 33 + l32] = 0.f;
+        for (int m = 0; m < 16; ++m) TF[(m * 2 + h) * 33 + l32] = 0.f;
         wave_lds_sync();
         // level 0: four 8x8 diagonal blocks, one column per lane (lanes 0..31)
         if (h == 0) {
@@ -325,11 +373,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
           for (int i = 1; i < 8; ++i) {
             float sacc = 0.f;
 #pragma unroll
-            for (int j = 0; j < i; ++j) sacc = __builtin_fmaf(Af[(o + i) * 33 + o + j], x[j], sacc);
+            for (int j = 0; j < i; ++j) sacc = __builtin_fmaf(AF[(o + i) * 33 + o + j], x[j], sacc);
             if (i > cc) x[i] = -sacc;
           }
 #pragma unroll
-          for (int i = 0; i < 8; ++i) Tf[(o + i) * 33 + o + cc] = x[i];
+          for (int i = 0; i < 8; ++i) TF[(o + i) * 33 + o + cc] = x[i];
         }
         wave_lds_sync();
         // level 1: T[m+1][m] = -D[m+1] A[m+1][m] D[m] for the three sub-diagonal 8x8 blocks
@@ -341,23 +389,22 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
             float sacc = 0.f;
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk)
-              sacc = __builtin_fmaf(Af[(8 * (m + 1) + ii) * 33 + 8 * m + kk], Tf[(8 * m + kk) * 33 + 8 * m + jj], sacc);
+              sacc = __builtin_fmaf(AF[(8 * (m + 1) + ii) * 33 + 8 * m + kk], TF[(8 * m + kk) * 33 + 8 * m + jj], sacc);
             y[m] = sacc;
           }
 #pragma unroll
-          for (int m = 0; m < 3; ++m) Yf[m * 64 + ii * 8 + jj] = y[m];
+          for (int m = 0; m < 3; ++m) YF[m * 64 + ii * 8 + jj] = y[m];
           wave_lds_sync();
 #pragma unroll
           for (int m = 0; m < 3; ++m) {
             float sacc = 0.f;
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk)
-              sacc = __builtin_fmaf(Tf[(8 * (m + 1) + ii) * 33 + 8 * (m + 1) + kk], Yf[m * 64 + kk * 8 + jj], sacc);
+              sacc = __builtin_fmaf(TF[(8 * (m + 1) + ii) * 33 + 8 * (m + 1) + kk], YF[m * 64 + kk * 8 + jj], sacc);
             y[m] = -sacc;
           }
-          wave_lds_sync();  // every lane has read Yf and the diagonal blocks
 #pragma unroll
-          for (int m = 0; m < 3; ++m) Tf[(8 * (m + 1) + ii) * 33 + 8 * m + jj] = y[m];
+          for (int m = 0; m < 3; ++m) TF[(8 * (m + 1) + ii) * 33 + 8 * m + jj] = y[m];
         }
         wave_lds_sync();
         // level 2: T[16:32][0:16] = -T16_1 A[16:32][0:16] T16_0
@@ -366,38 +413,33 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
           float y[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int kk = 0; kk < 16; ++kk) {
-            const float av = Af[(16 + ii) * 33 + kk];
+            const float av = AF[(16 + ii) * 33 + kk];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] = __builtin_fmaf(av, Tf[kk * 33 + j4 + q], y[q]);
+            for (int q = 0; q < 4; ++q) y[q] = __builtin_fmaf(av, TF[kk * 33 + j4 + q], y[q]);
           }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) Yf[ii * 17 + j4 + q] = y[q];
+          for (int q = 0; q < 4; ++q) YF[ii * 17 + j4 + q] = y[q];
           wave_lds_sync();
           float z[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int kk = 0; kk < 16; ++kk) {
-            const float tv = Tf[(16 + ii) * 33 + 16 + kk];
+            const float tv = TF[(16 + ii) * 33 + 16 + kk];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) z[q] = __builtin_fmaf(tv, Yf[kk * 17 + j4 + q], z[q]);
+            for (int q = 0; q < 4; ++q) z[q] = __builtin_fmaf(tv, YF[kk * 17 + j4 + q], z[q]);
           }
-          wave_lds_sync();
 #pragma unroll
-          for (int q = 0; q < 4; ++q) Tf[(16 + ii) * 33 + j4 + q] = -z[q];
+          for (int q = 0; q < 4; ++q) TF[(16 + ii) * 33 + j4 + q] = -z[q];
         }
         wave_lds_sync();
         // scaled operand copies: T1 = T diag(beta e^gamma), T2 = T diag(beta)
         {
-          const float* bet = BET(gs);
-          const float* eg = EG(gs);
-          OpT* t1 = T1(gs);
-          OpT* t2 = T2(gs);
-          const float bj = bet[l32], bej = bet[l32] * eg[l32];
+          const float bj = BET[l32], bej = BET[l32] * EG[l32];
 #pragma unroll
           for (int m = 0; m < 16; ++m) {
             const int i = 2 * m + h;
-            const float tv = (l32 <= i) ? Tf[i * 33 + l32] : 0.f;
-            t1[i * TROW + l32] = from_f32<OpT>(tv * bej);
-            t2[i * TROW + l32] = from_f32<OpT>(tv * bj);
+            const float tv = (l32 <= i) ? TF[i * 33 + l32] : 0.f;
+            T1[i * TROW + l32] = from_f32<OpT>(tv * bej);
+            T2[i * TROW + l32] = from_f32<OpT>(tv * bj);
           }
         }
       }
@@ -405,77 +447,73 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
     __syncthreads();
 
     // ------------------------------------------------------------------ W phase: W = T1 K^
-    {
-      constexpr int NT = NS * KT;
+    if (u < KT) {
+      const int kt = u;
+      F fa, fb;
+      lds_frag(T1 + l32 * TROW, h, fa);
+      lds_frag(KTr + (kt * 32 + l32) * TROW, h, fb);
+      f32x16 acc = zero16();
+      mma32(acc, fa, fb);
 #pragma unroll
-      for (int id0 = 0; id0 < NT; id0 += 4) {
-        const int id = id0 + wave;
-        if (id < NT) {
-          const int s = id / KT, kt = id % KT;
-          F fa, fb;
-          lds_frag(T1(s) + l32 * TROW, h, fa);
-          lds_frag(KTr(s) + (kt * 32 + l32) * TROW, h, fb);
-          f32x16 acc = zero16();
-          mma32(acc, fa, fb);
-          OpT* W = KH(s);  // K^ row-major is dead after the G phase
-#pragma unroll
-          for (int v = 0; v < 16; ++v) W[rho(v, h) * QROW + kt * 32 + l32] = from_f32<OpT>(acc[v]);
-        }
-      }
+      for (int v = 0; v < 16; ++v) KH[rho(v, h) * QROW + kt * 32 + l32] = from_f32<OpT>(acc[v]);  // K^ is dead
     }
     __syncthreads();
 
     // ------------------------------------------------------------------ state phase
-    if (role == 0 || FORK) {
-      const int s = role;  // stream
-      const int sbuf = FORK ? (c & 1) : 0;
+    if (state_wave) {
       f32x16 accU = zero16(), accWS = zero16(), accQS = zero16();
       {
         F fa, fb;
-        lds_frag(T2(s) + l32 * TROW, h, fa);
-        lds_frag(VT(s) + (my_sl * 32 + l32) * TROW, h, fb);
+        lds_frag(T2 + l32 * TROW, h, fa);
+        lds_frag(VT + (u * 32 + l32) * TROW, h, fb);
         mma32(accU, fa, fb);
       }
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
-        F fw, fq;
-        lds_frag(KH(s) + l32 * QROW + kt * 32, h, fw);
-        lds_frag(QH(s) + l32 * QROW + kt * 32, h, fq);
-        const F sx = *SBUF(sbuf, my_sl, kt);
+        F fw, fq, sx;
+        lds_frag(KH + l32 * QROW + kt * 32, h, fw);
+        lds_frag(QH + l32 * QROW + kt * 32, h, fq);
+        if constexpr (FORK) {
+          sx = *SBUF(u, kt);
+        } else {
+          acc_to_frag(S[kt], sx);
+        }
         mma32(accWS, fw, sx);
         mma32(accQS, fq, sx);
       }
-      const float* eg = EG(s);
       f32x16 vn;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         vn[v] = accU[v] - accWS[v];
-        accQS[v] *= eg[rho(v, h)];
+        accQS[v] *= EG[rho(v, h)];
       }
-      F fv;
-      acc_to_frag(vn, fv);
       {
-        F fp;
-        lds_frag(PP(s) + l32 * TROW, h, fp);
+        F fv, fp;
+        acc_to_frag(vn, fv);
+        lds_frag(PP + l32 * TROW, h, fp);
         mma32(accQS, fp, fv);
       }
-      // output rows of the real tokens
-      if (col_ok) {
-        const long long rs = (long long)a.Hv * a.Dv;  // token stride of out
-        OpT* ob = (OpT*)a.s[s].out + ((long long)b * a.T + t0) * rs + (long long)hv * a.Dv + col0 + my_sl * 32;
-        const unsigned lo = (unsigned)(4 * h) * (unsigned)rs + (unsigned)l32;
+      // output rows of the real tokens: uniform row bases, one 32-bit lane offset
+      {
+        const int rs = opaque(a.Hv * a.Dv);  // token stride of out
+        OpT* ob = (OpT*)st.out + ((long long)b * a.T + t0) * rs + (long long)hv * a.Dv + scol0;
+        const unsigned lo = (unsigned)(4 * h * rs + l32);
+        if (a.sub == 32 && slice_full) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int ru = ((v >> 2) << 3) + (v & 3);  // row = ru + 4h
-          if (ru + 4 * h < a.sub) (ob + ru * rs)[lo] = from_f32<OpT>(accQS[v]);
+          for (int v = 0; v < 16; ++v) (ob + (((v >> 2) << 3) + (v & 3)) * rs)[lo] = from_f32<OpT>(accQS[v]);
+        } else if (col_ok) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int ru = ((v >> 2) << 3) + (v & 3);  // row = ru + 4h
+            if (ru + 4 * h < a.sub) (ob + ru * rs)[lo] = from_f32<OpT>(accQS[v]);
+          }
         }
       }
-      if (role == 0) {
-        const float* egl = EGL(s);
-        const float lam = eg[31];
+      if (set == 0) {
+        const float lam = EG[31];
         f32x16 vd;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) vd[v] = vn[v] * egl[rho(v, h)];
+        for (int v = 0; v < 16; ++v) vd[v] = vn[v] * EGL[rho(v, h)];
         F fd;
         acc_to_frag(vd, fd);
 #pragma unroll
@@ -483,64 +521,79 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnArgs a) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) S[kt][v] *= lam;
           F fk;
-          lds_frag(KTr(s) + (kt * 32 + l32) * TROW, h, fk);
+          lds_frag(KTr + (kt * 32 + l32) * TROW, h, fk);
           mma32(S[kt], fk, fd);
         }
-        if (a.states && ((c + 1) % a.snap_every) == 0 && col_ok) {
+        if (a.states && ((c + 1) % a.snap_every) == 0) {
           const int sn = (c + 1) / a.snap_every - 1;
-          float* sb = a.states + (((long long)b * nsnap + sn) * a.Hv + hv) * (long long)a.Dk * a.Dv + col0 + my_sl * 32;
-          const unsigned lo = (unsigned)(4 * h * a.Dv + l32);
+          float* sb = a.states + (((long long)b * nsnap + sn) * a.Hv + hv) * (long long)a.Dk * a.Dv + scol0;
+          const int dv = opaque(a.Dv);
+          if (a.Dk == DK && dv == DVW) {  // full head: compile-time row stride, immediate offsets
+            float* lp = sb + 4 * h * DVW + l32;
 #pragma unroll
-          for (int kt = 0; kt < KT; ++kt)
+            for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int du = 32 * kt + ((v >> 2) << 3) + (v & 3);  // dk = du + 4h
-              if (du + 4 * h < a.Dk) __builtin_nontemporal_store(S[kt][v], (sb + (long long)du * a.Dv) + lo);
-            }
-        }
+              for (int v = 0; v < 16; ++v)
+                __builtin_nontemporal_store(S[kt][v], lp + (32 * kt + ((v >> 2) << 3) + (v & 3)) * DVW);
+          } else if (col_ok) {
+            const unsigned lo = (unsigned)(4 * h * dv + l32);
 #pragma unroll
-        for (int t = 0; t < KT; ++t) {
-          F f;
-          acc_to_frag(S[t], f);
-          *SBUF(FORK ? ((c + 1) & 1) : 0, my_sl, t) = f;
+            for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const int du = 32 * kt + ((v >> 2) << 3) + (v & 3);  // dk = du + 4h
+                if (du + 4 * h < a.Dk) __builtin_nontemporal_store(S[kt][v], (sb + (long long)du * dv) + lo);
+              }
+          }
         }
       }
     }
   }
 }
 
-template <int DK, bool BF16, bool FORK>
+template <int DK, int DVW, bool BF16, bool FORK>
 static int launch_gdn(const GdnArgs& a, hipStream_t st) {
-  const int nsl = (a.Dv + 63) / 64;
-  const long long nblk = (long long)a.B * a.Hv * nsl;
+  const int nwin = (a.Dv + DVW - 1) / DVW;
+  const long long nblk = (long long)a.B * a.Hv * nwin;
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "gdn: grid too large");
-  gdn_chunk_kernel<DK, BF16, FORK><<<dim3((unsigned)nblk), dim3(256), 0, st>>>(a);
+  gdn_chunk_kernel<DK, DVW, BF16, FORK><<<dim3((unsigned)nblk), dim3(FORK ? 512 : 256), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "gdn launch: %s", hipGetErrorString(e));
   return DLLM_OK;
 }
 
 static int gcd_int(int x, int y) {
-  while (y) { int t = x % y; x = y; y = t; }
+  while (y) {
+    int t = x % y;
+    x = y;
+    y = t;
+  }
   return x;
 }
 
+// Column window per workgroup: bf16 covers the whole value head (up to 128 columns, one workgroup
+// per (b, head)); fp32 operands take twice the LDS, so fp32 uses 64-column windows.
+static int window_for(int dtype) { return dtype == DT_BF16 ? 128 : 64; }
+
 static int dispatch_gdn(GdnArgs& a, int dtype, bool fork, hipStream_t st) {
-  const int dk = a.Dk <= 64 ? 64 : 128;
   if (a.Dk > 128) return fail(DLLM_EUNSUPPORTED, "gdn: Dk=%d > 128 not supported", a.Dk);
+  if (a.Dv > 128) return fail(DLLM_EUNSUPPORTED, "gdn: Dv=%d > 128 not supported", a.Dv);
+  const int dk = a.Dk <= 64 ? 64 : 128;
   if (dtype == DT_BF16) {
-    if (dk == 64) return fork ? launch_gdn<64, true, true>(a, st) : launch_gdn<64, true, false>(a, st);
-    return fork ? launch_gdn<128, true, true>(a, st) : launch_gdn<128, true, false>(a, st);
+    if (dk == 64) return fork ? launch_gdn<64, 128, true, true>(a, st) : launch_gdn<64, 128, true, false>(a, st);
+    return fork ? launch_gdn<128, 128, true, true>(a, st) : launch_gdn<128, 128, true, false>(a, st);
   }
   if (dtype == DT_F32) {
-    if (dk == 64) return fork ? launch_gdn<64, false, true>(a, st) : launch_gdn<64, false, false>(a, st);
+    if (dk == 64) return fork ? launch_gdn<64, 64, false, true>(a, st) : launch_gdn<64, 64, false, false>(a, st);
     if (fork) return fail(DLLM_EUNSUPPORTED, "gdn: fused fork needs Dk<=64 in fp32 (use the two-pass fork)");
-    return launch_gdn<128, false, false>(a, st);
+    return launch_gdn<128, 64, false, false>(a, st);
   }
   return fail(DLLM_EUNSUPPORTED, "gdn: dtype %d not supported", dtype);
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+static bool fits_i32(long long x) { return x >= -2147483647LL && x <= 2147483647LL; }
 
 }  // namespace dllm
 
@@ -564,14 +617,21 @@ extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const
     return fail(DLLM_EINVAL, "gdn: bad sizes B=%d T=%d Hk=%d Hv=%d Dk=%d Dv=%d chunk=%d", B, T, Hk, Hv, Dk, Dv, chunk);
   if (T % chunk) return fail(DLLM_EINVAL, "sequence_length %d is not a multiple of chunk_size %d", T, chunk);
   if (Hv % Hk) return fail(DLLM_EINVAL, "gdn: Hv=%d is not a multiple of Hk=%d", Hv, Hk);
+  const int64_t* sts[5] = {q_strides, k_strides, v_strides, beta_strides, g_strides};
+  const int H[5] = {Hk, Hk, Hv, Hv, Hv};
+  for (int i = 0; i < 5; ++i)
+    if (!fits_i32((long long)T * sts[i][1]) || !fits_i32((long long)H[i] * sts[i][2]) ||
+        !fits_i32((long long)T * sts[i][1] + (long long)H[i] * sts[i][2]))
+      return fail(DLLM_EUNSUPPORTED, "gdn: per-sequence extent exceeds 32-bit element offsets");
   GdnArgs a = {};
   GdnStream& s = a.s[0];
   s.q = q; s.k = k; s.v = v; s.g = g; s.beta = beta; s.out = out;
-  s.q_sb = q_strides[0]; s.q_st = q_strides[1]; s.q_sh = q_strides[2];
-  s.k_sb = k_strides[0]; s.k_st = k_strides[1]; s.k_sh = k_strides[2];
-  s.v_sb = v_strides[0]; s.v_st = v_strides[1]; s.v_sh = v_strides[2];
-  s.g_sb = g_strides[0]; s.g_st = g_strides[1]; s.g_sh = g_strides[2];
-  s.b_sb = beta_strides[0]; s.b_st = beta_strides[1]; s.b_sh = beta_strides[2];
+  a.q_sb = q_strides[0]; a.q_st = (int)q_strides[1]; a.q_sh = (int)q_strides[2];
+  a.k_sb = k_strides[0]; a.k_st = (int)k_strides[1]; a.k_sh = (int)k_strides[2];
+  a.v_sb = v_strides[0]; a.v_st = (int)v_strides[1]; a.v_sh = (int)v_strides[2];
+  a.g_sb = g_strides[0]; a.g_st = (int)g_strides[1]; a.g_sh = (int)g_strides[2];
+  a.b_sb = beta_strides[0]; a.b_st = (int)beta_strides[1]; a.b_sh = (int)beta_strides[2];
+  a.s[1] = a.s[0];
   a.init = initial_state;
   a.states = states;
   a.B = B; a.T = T; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv;
@@ -584,7 +644,7 @@ extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const
   auto st_ok = [&](const int64_t* st3) { return (st3[0] % vel == 0) && (st3[1] % vel == 0) && (st3[2] % vel == 0); };
   const int dkw = Dk <= 64 ? 64 : 128;
   a.vec_qk = aligned16(q) && aligned16(k) && st_ok(q_strides) && st_ok(k_strides) && Dk == dkw;
-  a.vec_v = aligned16(v) && st_ok(v_strides) && (Dv % 64 == 0);
+  a.vec_v = aligned16(v) && st_ok(v_strides) && (Dv % window_for(dtype) == 0);
   return dispatch_gdn(a, dtype, false, (hipStream_t)stream);
 }
 
@@ -599,6 +659,8 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
   if (Hv % Hk) return fail(DLLM_EINVAL, "gdn fork: Hv=%d is not a multiple of Hk=%d", Hv, Hk);
   if (!dllm_gdn_fused_fork_supported(Dk, block, dtype))
     return fail(DLLM_EUNSUPPORTED, "gdn fork: fused fork unsupported for Dk=%d block=%d dtype=%d", Dk, block, dtype);
+  if (!fits_i32((long long)L * qkv_stride_t) || !fits_i32((long long)L * Hv))
+    return fail(DLLM_EUNSUPPORTED, "gdn fork: per-sequence extent exceeds 32-bit element offsets");
   GdnArgs a = {};
   const int esz = dtype == DT_BF16 ? 2 : 4;
   const char* base[2] = {(const char*)qkv0, (const char*)qkvt};
@@ -610,14 +672,17 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
     s.q = base[i];
     s.k = base[i] + (long long)Hk * Dk * esz;
     s.v = base[i] + 2LL * Hk * Dk * esz;
-    s.q_sb = s.k_sb = s.v_sb = qkv_stride_b;
-    s.q_st = s.k_st = s.v_st = qkv_stride_t;
-    s.q_sh = s.k_sh = Dk;
-    s.v_sh = Dv;
-    s.beta = bet[i]; s.b_sb = (long long)L * Hv; s.b_st = Hv; s.b_sh = 1;
-    s.g = gg[i]; s.g_sb = (long long)L * Hv; s.g_st = Hv; s.g_sh = 1;
+    s.beta = bet[i];
+    s.g = gg[i];
     s.out = outs[i];
   }
+  a.q_sb = a.k_sb = a.v_sb = qkv_stride_b;
+  a.q_st = a.k_st = a.v_st = (int)qkv_stride_t;
+  a.q_sh = a.k_sh = Dk;
+  a.v_sh = Dv;
+  a.b_sb = a.g_sb = (long long)L * Hv;
+  a.b_st = a.g_st = Hv;
+  a.b_sh = a.g_sh = 1;
   a.init = nullptr;
   a.states = states;
   a.B = B; a.T = L; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv;
@@ -630,6 +695,6 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
                      ((long long)Hk * Dk % vel == 0);
   const int dkw = Dk <= 64 ? 64 : 128;
   a.vec_qk = aligned16(qkv0) && aligned16(qkvt) && st_ok && Dk == dkw;
-  a.vec_v = aligned16(qkv0) && aligned16(qkvt) && st_ok && (Dv % 64 == 0);
+  a.vec_v = aligned16(qkv0) && aligned16(qkvt) && st_ok && (Dv % window_for(dtype) == 0);
   return dispatch_gdn(a, dtype, true, (hipStream_t)stream);
 }

@@ -90,10 +90,11 @@ struct GdnSmem {
   static constexpr int O_T1 = O_P + 32 * TROW * (int)sizeof(OpT);
   static constexpr int O_T2 = O_T1 + 32 * TROW * (int)sizeof(OpT);
   static constexpr int O_AF = O_T2 + 32 * TROW * (int)sizeof(OpT);
-  static constexpr int O_TF = O_AF + 32 * 33 * 4;
-  static constexpr int O_YF = O_TF + 32 * 33 * 4;
-  static constexpr int O_VEC = O_YF + 16 * 17 * 4;  // gam, bet, eg, egl (32 floats each)
-  static constexpr int STREAM_BYTES = ((O_VEC + 4 * 32 * 4) + 15) & ~15;
+  static constexpr int FROW = 36;  // fp32 [32][32] scratch row stride (16-byte aligned rows)
+  static constexpr int O_TF = O_AF + 32 * FROW * 4;
+  static constexpr int O_YF = O_TF + 32 * FROW * 4;
+  static constexpr int O_VEC = O_YF + 16 * 20 * 4;  // eight per-row vectors of 32 floats
+  static constexpr int STREAM_BYTES = ((O_VEC + 8 * 32 * 4) + 15) & ~15;
   static constexpr int FRAG_BYTES = 16 * (int)sizeof(OpT);
   // state operand fragments published by the clean set for the noised set: [NSL][KT][64 lanes]
   static constexpr int O_SB = NS * STREAM_BYTES;
@@ -147,6 +148,8 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
   constexpr int NSL = SM::NSL;
   constexpr int QROW = SM::QROW;
   constexpr int TROW = SM::TROW;
+  constexpr int FROW = SM::FROW;
+  constexpr float LOG2E = 1.4426950408889634f;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
 
   const int tid = threadIdx.x;
@@ -167,20 +170,24 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
   const int nsnap = a.T / (a.sub * a.snap_every);
 
   unsigned char* sbase = smem + set * SM::STREAM_BYTES;
-  OpT* const QH = (OpT*)(sbase + SM::O_QH);
-  OpT* const KH = (OpT*)(sbase + SM::O_KH);
-  OpT* const KTr = (OpT*)(sbase + SM::O_KT);
-  OpT* const VT = (OpT*)(sbase + SM::O_VT);
-  OpT* const PP = (OpT*)(sbase + SM::O_P);
-  OpT* const T1 = (OpT*)(sbase + SM::O_T1);
-  OpT* const T2 = (OpT*)(sbase + SM::O_T2);
+  OpT* const QH = (OpT*)(sbase + SM::O_QH);    // raw q rows            [32][DK]
+  OpT* const KH = (OpT*)(sbase + SM::O_KH);    // raw k rows, then W    [32][DK]
+  OpT* const KTr = (OpT*)(sbase + SM::O_KT);   // raw k transposed      [DK][32]
+  OpT* const VT = (OpT*)(sbase + SM::O_VT);    // raw v transposed      [DVW][32]
+  OpT* const PP = (OpT*)(sbase + SM::O_P);     // P with q row norms    [32][32]
+  OpT* const T1 = (OpT*)(sbase + SM::O_T1);    // T diag(beta e^g rnk)  [32][32]
+  OpT* const T2 = (OpT*)(sbase + SM::O_T2);    // T diag(beta)          [32][32]
   float* const AF = (float*)(sbase + SM::O_AF);
   float* const TF = (float*)(sbase + SM::O_TF);
   float* const YF = (float*)(sbase + SM::O_YF);
-  float* const GAM = (float*)(sbase + SM::O_VEC);
-  float* const BET = GAM + 32;
-  float* const EG = GAM + 64;
-  float* const EGL = GAM + 96;
+  float* const GAML = (float*)(sbase + SM::O_VEC);  // cumulative decay, log2 units
+  float* const BET = GAML + 32;                     // beta
+  float* const EG = GAML + 64;                      // e^gamma
+  float* const EGL = GAML + 96;                     // e^(gamma_last - gamma)
+  float* const RNK = GAML + 128;                    // 1/||k|| (1 without l2norm)
+  float* const RNQ = GAML + 160;                    // scale/||q||
+  float* const EGQ = GAML + 192;                    // e^gamma scale/||q||
+  float* const EGLK = GAML + 224;                   // e^(gamma_last - gamma)/||k||
   auto SBUF = [&](int sl, int kt) { return (F*)(smem + SM::O_SB) + ((sl * KT + kt) * 64 + lane); };
 
   // this set's stream: base pointers at (b, head)
@@ -250,55 +257,64 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
     }
   };
   issue_loads(0);
+  const V16 vzero = {};
 
   for (int c = 0; c < ntiles; ++c) {
     const int t0 = c * a.sub;
     __syncthreads();  // the previous tile's state phase is done with every LDS operand
 
     // ------------------------------------------------------------------ load phase (registers -> LDS)
+    // Raw q, k, v are stored as loaded (exact); the l2 norms are applied as row/column scalings
+    // of the products. Padding rows store zeros.
     {
-      float x[NE];
+      V16 xq[NE / EPV], xk[NE / EPV], xv[NV / EPV];
 #pragma unroll
-      for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rq[i / EPV][i % EPV]) : 0.f;
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
-      ss = dpp_sum8(ss);
-      float rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-#pragma unroll
-      for (int i = 0; i < NE / 2; ++i) {
-        QH[lr * QROW + qe0 + i] = from_f32<OpT>((x[i] * rn) * a.scale);
-        QH[lr * QROW + qe1 + i] = from_f32<OpT>((x[NE / 2 + i] * rn) * a.scale);
+      for (int i = 0; i < NE / EPV; ++i) {
+        xq[i] = lreal ? rq[i] : vzero;
+        xk[i] = lreal ? rk[i] : vzero;
       }
 #pragma unroll
-      for (int i = 0; i < NE; ++i) x[i] = lreal ? to_f32(rk[i / EPV][i % EPV]) : 0.f;
-      ss = 0.f;
+      for (int i = 0; i < NV / EPV; ++i) xv[i] = lreal ? rv[i] : vzero;
+      constexpr int HV = TWO_QK ? NE / 2 / EPV : 1;  // vectors per q/k run (single run: 1)
+      if constexpr (TWO_QK) {
 #pragma unroll
-      for (int i = 0; i < NE; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
-      ss = dpp_sum8(ss);
-      rn = a.l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
+        for (int i = 0; i < HV; ++i) {
+          *(V16*)(QH + lr * QROW + qe0 + i * EPV) = xq[i];
+          *(V16*)(QH + lr * QROW + qe1 + i * EPV) = xq[HV + i];
+          *(V16*)(KH + lr * QROW + qe0 + i * EPV) = xk[i];
+          *(V16*)(KH + lr * QROW + qe1 + i * EPV) = xk[HV + i];
+        }
+      } else {
+        *(V16*)(QH + lr * QROW + qe0) = xq[0];
+        *(V16*)(KH + lr * QROW + qe0) = xk[0];
+      }
 #pragma unroll
       for (int i = 0; i < NE / 2; ++i) {
-        const OpT y0 = from_f32<OpT>(x[i] * rn);
-        const OpT y1 = from_f32<OpT>(x[NE / 2 + i] * rn);
-        KH[lr * QROW + qe0 + i] = y0;
-        KH[lr * QROW + qe1 + i] = y1;
-        KTr[(qe0 + i) * TROW + lr] = y0;
-        KTr[(qe1 + i) * TROW + lr] = y1;
+        KTr[(qe0 + i) * TROW + lr] = xk[i / EPV][i % EPV];
+        KTr[(qe1 + i) * TROW + lr] = xk[(NE / 2 + i) / EPV][(NE / 2 + i) % EPV];
       }
 #pragma unroll
       for (int i = 0; i < NV / 2; ++i) {
-        VT[(ve0 + i) * TROW + lr] = lreal ? rv[i / EPV][i % EPV] : from_f32<OpT>(0.f);
-        VT[(ve1 + i) * TROW + lr] = lreal ? rv[(NV / 2 + i) / EPV][(NV / 2 + i) % EPV] : from_f32<OpT>(0.f);
+        VT[(ve0 + i) * TROW + lr] = xv[i / EPV][i % EPV];
+        VT[(ve1 + i) * TROW + lr] = xv[(NV / 2 + i) / EPV][(NV / 2 + i) % EPV];
       }
+      // q row norm (the k norms come from the diagonal of K K^T)
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        const float x = to_f32(xq[i / EPV][i % EPV]);
+        ss = __builtin_fmaf(x, x, ss);
+      }
+      ss = dpp_sum8(ss);
+      if (lseg == 0) RNQ[lr] = a.l2norm ? a.scale * rsqrtf(ss + 1e-6f) : a.scale;
       // beta, g and the cumulative decay in sequential order (as a cumsum), one wave per set
       if (u == 0) {
-        if (h == 0) GAM[l32] = rg;
+        if (h == 0) GAML[l32] = rg;
         wave_lds_sync();
         float gam = 0.f, gall = 0.f;
 #pragma unroll
         for (int q = 0; q < 32; q += 4) {
-          const f32x4 g4 = *(const f32x4*)(GAM + q);
+          const f32x4 g4 = *(const f32x4*)(GAML + q);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             if (q + e <= l32) gam += g4[e];
@@ -307,10 +323,10 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         }
         wave_lds_sync();
         if (h == 0) {
-          GAM[l32] = gam;
+          GAML[l32] = gam * LOG2E;
           BET[l32] = rb;
-          EG[l32] = expf(gam);
-          EGL[l32] = expf(gall - gam);
+          EG[l32] = __builtin_amdgcn_exp2f(gam * LOG2E);
+          EGL[l32] = __builtin_amdgcn_exp2f((gall - gam) * LOG2E);
         }
       }
       // the clean set publishes the state before this tile for the noised set
@@ -328,125 +344,190 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
     __syncthreads();
     if (c + 1 < ntiles) issue_loads(t0 + a.sub);  // next tile's inputs travel during this tile
 
-    // ------------------------------------------------------------------ G (+ T) phase
+    // ------------------------------------------------------------------ G phase + diagonal blocks of T
+    // (every step issues all of its LDS reads before computing: one LDS round trip per step)
     {
-      // Gram + T on waves 0 / 5 and QK^T on waves 2 / 7: four different SIMDs in fork mode
+      // K K^T (+ k norms, A, and the first two levels of T) on waves 0 / 5, Q K^T on waves 2 / 7:
+      // four different SIMDs in fork mode
       const bool isG = (u == (set == 0 ? 0 : 1));
       const bool isQK = (u == (set == 0 ? 2 : 3));
       if (isG || isQK) {
         const OpT* X = isG ? KH : QH;
-        f32x16 acc = zero16();
+        F fa[KT], fb[KT];
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
-          F fa, fb;
-          lds_frag(X + l32 * QROW + kt * 32, h, fa);
-          lds_frag(KH + l32 * QROW + kt * 32, h, fb);
-          mma32(acc, fa, fb);
+          lds_frag(X + l32 * QROW + kt * 32, h, fa[kt]);
+          lds_frag(KH + l32 * QROW + kt * 32, h, fb[kt]);
         }
-        const float gj = GAM[l32];
-        if (isG) {
+        f32x4 gam4[4];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int i = rho(v, h);
-            AF[i * 33 + l32] = (l32 < i) ? BET[i] * acc[v] * expf(GAM[i] - gj) : 0.f;
+        for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(GAML + 8 * m + 4 * h);
+        const float gj = GAML[l32];
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fb[kt]);
+        if (isG) {
+          // k norms from the diagonal of K K^T: lane (j, h = (j>>2)&1) holds element (j, j)
+          float dg = 0.f;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) dg = (rho(v, h) == l32) ? acc[v] : dg;
+          if (h == ((l32 >> 2) & 1)) RNK[l32] = a.l2norm ? rsqrtf(dg + 1e-6f) : 1.f;
+          wave_lds_sync();
+          f32x4 bet4[4], rnk4[4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            bet4[m] = *(const f32x4*)(BET + 8 * m + 4 * h);
+            rnk4[m] = *(const f32x4*)(RNK + 8 * m + 4 * h);
+          }
+          const float rj = RNK[l32];
+          const float eglj = EGL[l32];
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int i = 8 * m + 4 * h + e;
+              const float val = (bet4[m][e] * rnk4[m][e] * rj) * acc[4 * m + e] *
+                                __builtin_amdgcn_exp2f(gam4[m][e] - gj);
+              AF[i * FROW + l32] = (l32 < i) ? val : 0.f;
+            }
+          if (h == 0) EGLK[l32] = eglj * rj;
+          wave_lds_sync();
+          // level 0: four 8x8 diagonal blocks, one column per lane (lanes 0..31); lanes of odd
+          // blocks also clear the block above (read as zero by level 2)
+          if (h == 0) {
+            const int bb = l32 >> 3, cc = l32 & 7, o = 8 * bb;
+            f32x4 ar[8][2];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) {
+              ar[i][0] = *(const f32x4*)(AF + (o + i) * FROW + o);
+              ar[i][1] = *(const f32x4*)(AF + (o + i) * FROW + o + 4);
+            }
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+            for (int i = 1; i < 8; ++i) {
+              float sacc = 0.f;
+#pragma unroll
+              for (int j = 0; j < i; ++j) sacc = __builtin_fmaf(ar[i][j >> 2][j & 3], x[j], sacc);
+              if (i > cc) x[i] = -sacc;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) TF[(o + i) * FROW + o + cc] = x[i];
+            if (bb & 1) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) TF[(o - 8 + i) * FROW + o + cc] = 0.f;
+            }
+          }
+          wave_lds_sync();
+          // level 1: T[m+1][m] = -D[m+1] (A[m+1][m] D[m]) for the three sub-diagonal 8x8 blocks
+          {
+            const int ii = lane >> 3, jj = lane & 7;
+            f32x4 arow[3][2];
+            float dcol[3][8];
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              arow[m][0] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m);
+              arow[m][1] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m + 4);
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) dcol[m][kk] = TF[(8 * m + kk) * FROW + 8 * m + jj];
+            }
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              float sacc = 0.f;
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(arow[m][kk >> 2][kk & 3], dcol[m][kk], sacc);
+              YF[m * 64 + ii * 8 + jj] = sacc;
+            }
+            wave_lds_sync();
+            f32x4 drow[3][2];
+            float ycol[3][8];
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              drow[m][0] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1));
+              drow[m][1] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1) + 4);
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) ycol[m][kk] = YF[m * 64 + kk * 8 + jj];
+            }
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              float sacc = 0.f;
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(drow[m][kk >> 2][kk & 3], ycol[m][kk], sacc);
+              TF[(8 * (m + 1) + ii) * FROW + 8 * m + jj] = -sacc;
+            }
           }
         } else {
+          f32x4 rnq4[4];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int i = rho(v, h);
-            PP[i * TROW + l32] = from_f32<OpT>((l32 <= i) ? acc[v] * expf(GAM[i] - gj) : 0.f);
-          }
-        }
-      }
-      if (isG) {
-        // T = (I + A)^-1, fp32, inside this wavefront
+          for (int m = 0; m < 4; ++m) rnq4[m] = *(const f32x4*)(RNQ + 8 * m + 4 * h);
+          const float egj = EG[l32], rqj = RNQ[l32];
 #pragma unroll
-        for (int m = 0; m < 16; ++m) TF[(m * 2 + h) * 33 + l32] = 0.f;
-        wave_lds_sync();
-        // level 0: four 8x8 diagonal blocks, one column per lane (lanes 0..31)
-        if (h == 0) {
-          const int bb = l32 >> 3, cc = l32 & 7, o = 8 * bb;
-          float x[8];
+          for (int m = 0; m < 4; ++m)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) x[i] = (i == cc) ? 1.f : 0.f;
-#pragma unroll
-          for (int i = 1; i < 8; ++i) {
-            float sacc = 0.f;
-#pragma unroll
-            for (int j = 0; j < i; ++j) sacc = __builtin_fmaf(AF[(o + i) * 33 + o + j], x[j], sacc);
-            if (i > cc) x[i] = -sacc;
-          }
-#pragma unroll
-          for (int i = 0; i < 8; ++i) TF[(o + i) * 33 + o + cc] = x[i];
-        }
-        wave_lds_sync();
-        // level 1: T[m+1][m] = -D[m+1] A[m+1][m] D[m] for the three sub-diagonal 8x8 blocks
-        {
-          const int ii = lane >> 3, jj = lane & 7;
-          float y[3];
-#pragma unroll
-          for (int m = 0; m < 3; ++m) {
-            float sacc = 0.f;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
-              sacc = __builtin_fmaf(AF[(8 * (m + 1) + ii) * 33 + 8 * m + kk], TF[(8 * m + kk) * 33 + 8 * m + jj], sacc);
-            y[m] = sacc;
-          }
-#pragma unroll
-          for (int m = 0; m < 3; ++m) YF[m * 64 + ii * 8 + jj] = y[m];
-          wave_lds_sync();
-#pragma unroll
-          for (int m = 0; m < 3; ++m) {
-            float sacc = 0.f;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
-              sacc = __builtin_fmaf(TF[(8 * (m + 1) + ii) * 33 + 8 * (m + 1) + kk], YF[m * 64 + kk * 8 + jj], sacc);
-            y[m] = -sacc;
-          }
-#pragma unroll
-          for (int m = 0; m < 3; ++m) TF[(8 * (m + 1) + ii) * 33 + 8 * m + jj] = y[m];
-        }
-        wave_lds_sync();
-        // level 2: T[16:32][0:16] = -T16_1 A[16:32][0:16] T16_0
-        {
-          const int ii = lane >> 2, j4 = (lane & 3) * 4;
-          float y[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kk = 0; kk < 16; ++kk) {
-            const float av = AF[(16 + ii) * 33 + kk];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] = __builtin_fmaf(av, TF[kk * 33 + j4 + q], y[q]);
-          }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) YF[ii * 17 + j4 + q] = y[q];
-          wave_lds_sync();
-          float z[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kk = 0; kk < 16; ++kk) {
-            const float tv = TF[(16 + ii) * 33 + 16 + kk];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) z[q] = __builtin_fmaf(tv, YF[kk * 17 + j4 + q], z[q]);
-          }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) TF[(16 + ii) * 33 + j4 + q] = -z[q];
-        }
-        wave_lds_sync();
-        // scaled operand copies: T1 = T diag(beta e^gamma), T2 = T diag(beta)
-        {
-          const float bj = BET[l32], bej = BET[l32] * EG[l32];
-#pragma unroll
-          for (int m = 0; m < 16; ++m) {
-            const int i = 2 * m + h;
-            const float tv = (l32 <= i) ? TF[i * 33 + l32] : 0.f;
-            T1[i * TROW + l32] = from_f32<OpT>(tv * bej);
-            T2[i * TROW + l32] = from_f32<OpT>(tv * bj);
-          }
+            for (int e = 0; e < 4; ++e) {
+              const int i = 8 * m + 4 * h + e;
+              const float val = rnq4[m][e] * acc[4 * m + e] * __builtin_amdgcn_exp2f(gam4[m][e] - gj);
+              PP[i * TROW + l32] = from_f32<OpT>((l32 <= i) ? val : 0.f);
+            }
+          if (h == 0) EGQ[l32] = egj * rqj;
         }
       }
     }
     __syncthreads();
 
-    // ------------------------------------------------------------------ W phase: W = T1 K^
+    // ------------------------------------------------------------------ T level 2 (all waves of the set)
+    // T[16:32][0:16] = -T16_1 (A[16:32][0:16] T16_0); the final entries elsewhere are already in TF.
+    // Thread ts owns entry (ii, jj) of the 16x16 block and writes the scaled operand copies
+    // T1 = T diag(beta e^gamma / ||k||) and T2 = T diag(beta) for four entries.
+    const int ii = ts >> 4, jj = ts & 15;
+    {
+      f32x4 arow[4];
+      float tcol[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) arow[q] = *(const f32x4*)(AF + (16 + ii) * FROW + 4 * q);
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk) tcol[kk] = TF[kk * FROW + jj];
+      // rows 0..15 (all columns) and the T16_1 block are final: scaled copies now
+      const int i0 = ts >> 4, j0 = (ts & 15) * 2;  // rows 0..15, columns j0, j0+1
+      const int i1 = 16 + (ts >> 4), j1 = 16 + (ts & 15);  // T16_1 block
+      const f32x2 t0v = *(const f32x2*)(TF + i0 * FROW + j0);
+      const float t1v = TF[i1 * FROW + j1];
+      const f32x2 b0 = *(const f32x2*)(BET + j0), e0 = *(const f32x2*)(EG + j0), r0 = *(const f32x2*)(RNK + j0);
+      const float b1 = BET[j1], e1 = EG[j1], r1 = RNK[j1];
+      float y = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk) y = __builtin_fmaf(arow[kk >> 2][kk & 3], tcol[kk], y);
+      YF[ii * 20 + jj] = y;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float tv = (j0 + e <= i0) ? t0v[e] : 0.f;
+        T1[i0 * TROW + j0 + e] = from_f32<OpT>(tv * (b0[e] * e0[e] * r0[e]));
+        T2[i0 * TROW + j0 + e] = from_f32<OpT>(tv * b0[e]);
+      }
+      const float tv1 = (j1 <= i1) ? t1v : 0.f;
+      T1[i1 * TROW + j1] = from_f32<OpT>(tv1 * (b1 * e1 * r1));
+      T2[i1 * TROW + j1] = from_f32<OpT>(tv1 * b1);
+    }
+    __syncthreads();
+    {
+      f32x4 trow[4];
+      float ycol[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) trow[q] = *(const f32x4*)(TF + (16 + ii) * FROW + 16 + 4 * q);
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk) ycol[kk] = YF[kk * 20 + jj];
+      const float bj = BET[jj], ej = EG[jj], rj = RNK[jj];
+      float z = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk) z = __builtin_fmaf(trow[kk >> 2][kk & 3], ycol[kk], z);
+      const float tv = -z;
+      T1[(16 + ii) * TROW + jj] = from_f32<OpT>(tv * (bj * ej * rj));
+      T2[(16 + ii) * TROW + jj] = from_f32<OpT>(tv * bj);
+    }
+    __syncthreads();
+
+    // ------------------------------------------------------------------ W phase: W = T1 K_raw
     if (u < KT) {
       const int kt = u;
       F fa, fb;
@@ -455,7 +536,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
       f32x16 acc = zero16();
       mma32(acc, fa, fb);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) KH[rho(v, h) * QROW + kt * 32 + l32] = from_f32<OpT>(acc[v]);  // K^ is dead
+      for (int v = 0; v < 16; ++v) KH[rho(v, h) * QROW + kt * 32 + l32] = from_f32<OpT>(acc[v]);  // raw k is dead
     }
     __syncthreads();
 
@@ -468,28 +549,43 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         lds_frag(VT + (u * 32 + l32) * TROW, h, fb);
         mma32(accU, fa, fb);
       }
+      constexpr int KH2 = KT >= 2 ? KT / 2 : 1;  // fragment reads in batches of KH2 K-slices
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        F fw, fq, sx;
-        lds_frag(KH + l32 * QROW + kt * 32, h, fw);
-        lds_frag(QH + l32 * QROW + kt * 32, h, fq);
-        if constexpr (FORK) {
-          sx = *SBUF(u, kt);
-        } else {
-          acc_to_frag(S[kt], sx);
+      for (int k0 = 0; k0 < KT; k0 += KH2) {
+        F fw[KH2], fq[KH2], sx[KH2];
+#pragma unroll
+        for (int q = 0; q < KH2; ++q) {
+          lds_frag(KH + l32 * QROW + (k0 + q) * 32, h, fw[q]);
+          lds_frag(QH + l32 * QROW + (k0 + q) * 32, h, fq[q]);
+          if constexpr (FORK) {
+            sx[q] = *SBUF(u, k0 + q);
+          } else {
+            acc_to_frag(S[k0 + q], sx[q]);
+          }
         }
-        mma32(accWS, fw, sx);
-        mma32(accQS, fq, sx);
-      }
-      f32x16 vn;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        vn[v] = accU[v] - accWS[v];
-        accQS[v] *= EG[rho(v, h)];
+        for (int q = 0; q < KH2; ++q) {
+          mma32(accWS, fw[q], sx[q]);
+          mma32(accQS, fq[q], sx[q]);
+        }
+      }
+      // O = diag(e^gamma scale/||q||) Q_raw S + P (V' / ||k||)
+      f32x16 vn, vk;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const f32x4 egq = *(const f32x4*)(EGQ + 8 * m + 4 * h);
+        const f32x4 rnk = *(const f32x4*)(RNK + 8 * m + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * m + e;
+          vn[v] = accU[v] - accWS[v];
+          vk[v] = vn[v] * rnk[e];
+          accQS[v] *= egq[e];
+        }
       }
       {
         F fv, fp;
-        acc_to_frag(vn, fv);
+        acc_to_frag(vk, fv);
         lds_frag(PP + l32 * TROW, h, fp);
         mma32(accQS, fp, fv);
       }
@@ -510,19 +606,25 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         }
       }
       if (set == 0) {
+        // S <- e^gamma_last S + K_raw^T (e^(gamma_last - gamma) / ||k|| V')
         const float lam = EG[31];
         f32x16 vd;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) vd[v] = vn[v] * EGL[rho(v, h)];
+        for (int m = 0; m < 4; ++m) {
+          const f32x4 eglk = *(const f32x4*)(EGLK + 8 * m + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vd[4 * m + e] = vn[4 * m + e] * eglk[e];
+        }
         F fd;
         acc_to_frag(vd, fd);
+        F fk[KT];
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) lds_frag(KTr + (kt * 32 + l32) * TROW, h, fk[kt]);
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) S[kt][v] *= lam;
-          F fk;
-          lds_frag(KTr + (kt * 32 + l32) * TROW, h, fk);
-          mma32(S[kt], fk, fd);
+          mma32(S[kt], fk[kt], fd);
         }
         if (a.states && ((c + 1) % a.snap_every) == 0) {
           const int sn = (c + 1) / a.snap_every - 1;

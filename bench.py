@@ -72,6 +72,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-sample-L", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibration-copy-gib", type=float, default=0.0,
+                    help="after the timed steps, copy this many GiB device-to-device (the reference transfer "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the state-fork layer shards over (batch, value head) with no "
@@ -144,6 +147,13 @@ def main(argv=None):
         "wall_s_timed": wall,
         "cpu_baseline": None,
     }
+    if a.calibration_copy_gib > 0:
+        n = int(a.calibration_copy_gib * (1 << 28))
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(a.cpu_sample_L)
         res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]

@@ -1,0 +1,394 @@
+// Block-diffusion attention with the complementary [2L, 2L] mask (gfx950 / CDNA4).
+//
+// Sequence = cat([x_t, x_0]) of length 2L, blocks of C tokens, positions kept per half. Query i may
+// see key j iff (with qb, kb the blocks inside each half):
+//   x_t -> x_t : kb == qb   (kb <= qb under the "mask-leak" fault)
+//   x_t -> x_0 : kb <  qb
+//   x_0 -> x_0 : kb <= qb
+//   x_0 -> x_t : never
+// The mask is never materialised: a workgroup takes four 32-query tiles of one half and one query
+// head; it walks only the 32-key tiles that the union of its rows can see, and each wave skips the
+// tiles its own rows cannot see. With C = 32 every (32-query, 32-key) tile is entirely visible or
+// entirely hidden, so no element masks are evaluated; other block sizes and ragged lengths mask
+// elements on the partial tiles only.
+//
+// Per wave and key tile: S^T = K Q^T on MFMA (rows = keys, lane = query), online softmax in fp32
+// with exp2, P rounded to the input dtype, then O^T += V^T P^T on MFMA: the accumulator layout of
+// S^T is directly the B-operand layout of P^T, and each lane owns one query column of O^T, so the
+// softmax rescale is a per-lane scalar. K tiles are staged row-major and V tiles transposed in a
+// double-buffered LDS ring, the next tile's global loads travelling during the current compute.
+// GQA: query head h reads KV head h / (Hq / Hkv), no repeat_kv copy.
+#include <type_traits>
+
+#include "common.h"
+
+namespace dllm {
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;  // [B, 2L, Hq, d] contiguous
+  long long q_sb, k_sb, v_sb;
+  int q_st, q_sh, k_st, k_sh, v_st, v_sh;
+  int B, L, Hq, Hkv, d, C;
+  int leak;
+  float scale_log2e;  // softmax scale * log2(e)
+  int vec;            // 16-byte vector loads of q/k/v rows allowed
+};
+
+__device__ __forceinline__ int xcd_linear_id_attn(int bid, int n) {
+  const int q = n >> 3, r = n & 7, x = bid & 7, i = bid >> 3;
+  return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
+// visibility of key block kb of half kh from query block qb of half qh (0 = x_t, 1 = x_0)
+__device__ __forceinline__ bool visible(int qh, int qb, int kh, int kb, int leak) {
+  if (qh == 0) return kh == 0 ? (leak ? kb <= qb : kb == qb) : (kb < qb);
+  return kh == 1 && kb <= qb;
+}
+
+// any / all of the query-block range [q0, q1] x key-block range [k0, k1] visible
+__device__ __forceinline__ void classify(int qh, int q0, int q1, int kh, int k0, int k1, int leak, bool& any,
+                                         bool& all) {
+  if (qh == 1 && kh == 0) { any = all = false; return; }
+  if (qh == 0 && kh == 0 && !leak) {
+    any = (k0 <= q1) && (q0 <= k1);
+    all = (q0 == q1) && (k0 == k1) && (k0 == q0);
+    return;
+  }
+  if (qh == 0 && kh == 1) {  // kb < qb
+    any = k0 < q1;
+    all = k1 < q0;
+    return;
+  }
+  any = k0 <= q1;  // kb <= qb
+  all = k1 <= q0;
+}
+
+template <int D, bool BF16>
+struct AttnSmem {
+  using OpT = typename std::conditional<BF16, bf16, float>::type;
+  static constexpr int KROW = D + (BF16 ? 8 : 4);  // K tile [32][D]
+  static constexpr int VROW = 36;                    // V^T tile [D][32]
+  static constexpr int K_BYTES = 32 * KROW * (int)sizeof(OpT);
+  static constexpr int V_BYTES = D * VROW * (int)sizeof(OpT);
+  static constexpr int STAGE = K_BYTES + V_BYTES;
+  static constexpr int TOTAL = 2 * STAGE;
+};
+
+template <int D, bool BF16>
+__global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
+  using SM = AttnSmem<D, BF16>;
+  using OpT = typename SM::OpT;
+  using F = Frag<BF16>;
+  constexpr int DT = D / 32;
+  constexpr int KROW = SM::KROW, VROW = SM::VROW;
+  constexpr int EPV = 16 / (int)sizeof(OpT);  // elements per 16-byte vector
+  constexpr int CPR = D / EPV;                // 16-byte chunks per row
+  constexpr int CPT = CPR >= 8 ? CPR / 8 : 1;  // chunks per thread per tile (K or V); 8 threads per row
+  using V16 = typename std::conditional<BF16, bf16x8, f32x4>::type;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int L = a.L, C = a.C;
+  const int ntq = (L + 31) >> 5;  // 32-row tiles per half
+  const int ng = (ntq + 3) >> 2;  // groups of four tiles per half
+  const int rep = a.Hq / a.Hkv;
+
+  // work unit: longest first (tile group descending), then half, batch, KV head, query head in group
+  const int lin = xcd_linear_id_attn(blockIdx.x, gridDim.x);
+  const int per_g = 2 * a.B * a.Hkv * rep;
+  const int g = ng - 1 - lin / per_g;
+  int rem = lin % per_g;
+  const int qh = rem % 2;  // alternate halves so equal-work units sit together
+  rem /= 2;
+  const int hr = rem % rep;
+  rem /= rep;
+  const int hkv = rem % a.Hkv;
+  const int b = rem / a.Hkv;
+  const int hq = hkv * rep + hr;
+
+  // this wave's query rows [r0, r1) inside half qh; the workgroup's rows [g0, g1)
+  const int g0 = g * 128, g1 = min(L, g0 + 128);
+  const int r0 = g0 + wave * 32, r1 = min(L, r0 + 32);
+  const bool wave_live = r0 < L;
+  const int qb0 = r0 / C, qb1 = (max(r0, r1 - 1)) / C;
+  const int gqb0 = g0 / C, gqb1 = (g1 - 1) / C;
+
+  // key ranges of the workgroup, per half: [lo, hi) in tokens
+  int lo0, hi0, lo1, hi1;  // half 0 (x_t) and half 1 (x_0)
+  if (qh == 1) {
+    lo0 = hi0 = 0;
+    lo1 = 0;
+    hi1 = min(L, (gqb1 + 1) * C);
+  } else {
+    lo0 = a.leak ? 0 : gqb0 * C;
+    hi0 = min(L, (gqb1 + 1) * C);
+    lo1 = 0;
+    hi1 = min(L, gqb1 * C);
+  }
+  const int t0lo = lo0 >> 5, t0hi = (hi0 + 31) >> 5;  // x_t key tiles
+  const int t1lo = lo1 >> 5, t1hi = (hi1 + 31) >> 5;  // x_0 key tiles
+  const int n0 = hi0 > lo0 ? t0hi - t0lo : 0;
+  const int n1 = hi1 > lo1 ? t1hi - t1lo : 0;
+  const int ntiles = n0 + n1;  // x_0 tiles first, then x_t tiles
+  auto tile_pos = [&](int n, int& kh, int& j0) {
+    if (n < n1) { kh = 1; j0 = (t1lo + n) * 32; }
+    else { kh = 0; j0 = (t0lo + n - n1) * 32; }
+  };
+
+  const OpT* const qbase = (const OpT*)a.q + b * a.q_sb + (long long)hq * a.q_sh;
+  const OpT* const kbase = (const OpT*)a.k + b * a.k_sb + (long long)hkv * a.k_sh;
+  const OpT* const vbase = (const OpT*)a.v + b * a.v_sb + (long long)hkv * a.v_sh;
+
+  // Q^T fragments for this wave's 32 queries (lane = query, d in rho order), kept in registers
+  F qf[DT];
+  {
+    const int row = min(r0 + l32, L - 1);  // rows past L load a valid row and are never stored
+    const OpT* qp = qbase + (long long)(qh * L + row) * a.q_st;
+#pragma unroll
+    for (int s = 0; s < DT; ++s) {
+      if constexpr (BF16) {
+        bf16x4 r[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int d0 = 32 * s + 8 * m + 4 * h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[m][e] = (d0 + e < a.d) ? qp[d0 + e] : from_f32<OpT>(0.f);
+        }
+        qf[s].lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+        qf[s].hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int dd = 32 * s + rho(v, h);
+          qf[s].v[v] = dd < a.d ? qp[dd] : 0.f;
+        }
+      }
+    }
+  }
+
+  // key/value tile staging: thread -> (key row kr, chunks {kc + 8q}) of K and of V
+  const int kr = tid >> 3, kc = tid & 7;
+  V16 rk[CPT], rv[CPT];
+  const V16 vz = {};
+  auto load_tile = [&](int n) {
+    int kh, j0;
+    tile_pos(n, kh, j0);
+    const int key = j0 + kr;
+    const bool ok = key < L;
+    const int krow = kh * L + (ok ? key : 0);
+    const OpT* kp = kbase + (long long)krow * a.k_st;
+    const OpT* vp = vbase + (long long)krow * a.v_st;
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      if (kc + 8 * q >= CPR) continue;
+      const int e0 = (kc + 8 * q) * EPV;
+      if (a.vec) {
+        rk[q] = *(const V16*)(kp + e0);
+        rv[q] = *(const V16*)(vp + e0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          rk[q][e] = (e0 + e < a.d) ? kp[e0 + e] : from_f32<OpT>(0.f);
+          rv[q][e] = (e0 + e < a.d) ? vp[e0 + e] : from_f32<OpT>(0.f);
+        }
+      }
+    }
+  };
+  auto store_tile = [&](int n, int stage) {
+    int kh, j0;
+    tile_pos(n, kh, j0);
+    const bool ok = j0 + kr < L;
+    OpT* Ks = (OpT*)(smem + stage * SM::STAGE);
+    OpT* Vs = (OpT*)(smem + stage * SM::STAGE + SM::K_BYTES);
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      if (kc + 8 * q >= CPR) continue;
+      const int e0 = (kc + 8 * q) * EPV;
+      const V16 kx = ok ? rk[q] : vz;
+      const V16 vx = ok ? rv[q] : vz;
+      *(V16*)(Ks + kr * KROW + e0) = kx;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) Vs[(e0 + e) * VROW + kr] = vx[e];
+    }
+  };
+
+  f32x16 O[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) O[t] = zero16();
+  float mrow = -1e30f, lrow = 0.f;  // running max (log2 units) and sum of this lane's query
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0, 0);
+  }
+  __syncthreads();
+  for (int n = 0; n < ntiles; ++n) {
+    if (n + 1 < ntiles) load_tile(n + 1);
+    int kh, j0;
+    tile_pos(n, kh, j0);
+    const int kb0 = j0 / C, kb1 = (min(L, j0 + 32) - 1) / C;
+    bool any = false, all = false;
+    if (wave_live) classify(qh, qb0, qb1, kh, kb0, kb1, a.leak, any, all);
+    const bool ragged = (j0 + 32 > L) || (r1 - r0 < 32);
+    if (any) {
+      const OpT* Ks = (const OpT*)(smem + (n & 1) * SM::STAGE);
+      const OpT* Vs = (const OpT*)(smem + (n & 1) * SM::STAGE + SM::K_BYTES);
+      // S^T = K Q^T : rows = keys (rho order), lane = query
+      f32x16 st = zero16();
+      constexpr int KB = DT >= 4 ? 4 : DT;
+#pragma unroll
+      for (int s0 = 0; s0 < DT; s0 += KB) {
+        F kf[KB];
+#pragma unroll
+        for (int s = 0; s < KB; ++s) lds_frag(Ks + l32 * KROW + 32 * (s0 + s), h, kf[s]);
+#pragma unroll
+        for (int s = 0; s < KB; ++s) mma32(st, kf[s], qf[s0 + s]);
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;
+      if (!all || ragged) {
+        const int qi = r0 + l32;
+        const int qbl = qi / C;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int kj = j0 + rho(v, h);
+          const bool okk = kj < L && qi < L && visible(qh, qbl, kh, kj / C, a.leak);
+          st[v] = okk ? st[v] : -INFINITY;
+        }
+      }
+      float mx = st[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, st[v]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(mrow, mx);
+      const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+      float ps = 0.f;
+      f32x16 p;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        p[v] = __builtin_amdgcn_exp2f(st[v] - mnew);
+        ps += p[v];
+      }
+      ps += __shfl_xor(ps, 32);
+      lrow = lrow * alpha + ps;
+      mrow = mnew;
+      F pf;
+      acc_to_frag(p, pf);
+      // O^T += V^T P^T
+      constexpr int VB = DT >= 4 ? 4 : DT;
+#pragma unroll
+      for (int t0 = 0; t0 < DT; t0 += VB) {
+        F vf[VB];
+#pragma unroll
+        for (int t = 0; t < VB; ++t) lds_frag(Vs + (32 * (t0 + t) + l32) * VROW, h, vf[t]);
+#pragma unroll
+        for (int t = 0; t < VB; ++t) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) O[t0 + t][v] *= alpha;
+          mma32(O[t0 + t], vf[t], pf);
+        }
+      }
+    }
+    if (n + 1 < ntiles) store_tile(n + 1, (n + 1) & 1);
+    __syncthreads();
+  }
+
+  // O = (O^T)^T / l : lane = query row, four runs of four consecutive d per 32-slice
+  const int qi = r0 + l32;
+  if (wave_live && qi < L) {
+    const float inv = 1.f / lrow;
+    OpT* op = (OpT*)a.out + (((long long)b * 2 * L + qh * L + qi) * a.Hq + hq) * a.d;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int d0 = 32 * t + 8 * m + 4 * h;
+        if constexpr (BF16) {
+          if (d0 + 4 <= a.d && (a.d & 3) == 0) {
+            bf16x4 o4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = (bf16)(O[t][4 * m + e] * inv);
+            *(bf16x4*)(op + d0) = o4;
+            continue;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (d0 + e < a.d) op[d0 + e] = from_f32<OpT>(O[t][4 * m + e] * inv);
+      }
+  }
+}
+
+template <int D, bool BF16>
+static int launch_attn(const AttnArgs& a, hipStream_t st) {
+  const int ntq = (a.L + 31) / 32;
+  const int ng = (ntq + 3) / 4;
+  const long long nblk = (long long)ng * 2 * a.B * a.Hq;
+  if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "attention: grid too large");
+  bd_attn_kernel<D, BF16><<<dim3((unsigned)nblk), dim3(256), 0, st>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention launch: %s", hipGetErrorString(e));
+  return DLLM_OK;
+}
+
+static bool fits32(long long x) { return x >= -2147483647LL && x <= 2147483647LL; }
+
+}  // namespace dllm
+
+using namespace dllm;
+
+extern "C" int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                     const void* v, const int64_t* v_strides, void* out, int B, int L, int Hq, int Hkv,
+                                     int d, int block, float scale, int dtype, int flags, void* stream) {
+  if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides)
+    return fail(DLLM_EINVAL, "attention: null pointer");
+  if (B <= 0 || L <= 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || block <= 0)
+    return fail(DLLM_EINVAL, "attention: bad sizes B=%d L=%d Hq=%d Hkv=%d d=%d block=%d", B, L, Hq, Hkv, d, block);
+  if (L % block) return fail(DLLM_EINVAL, "L=%d is not a multiple of block=%d", L, block);
+  if (Hq % Hkv) return fail(DLLM_EINVAL, "attention: Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+  if (d > 256) return fail(DLLM_EUNSUPPORTED, "attention: head_dim %d > 256 not supported", d);
+  const int64_t* sts[3] = {q_strides, k_strides, v_strides};
+  const int H[3] = {Hq, Hkv, Hkv};
+  for (int i = 0; i < 3; ++i)
+    if (!fits32(2LL * L * sts[i][1]) || !fits32((long long)H[i] * sts[i][2]) ||
+        !fits32(2LL * L * sts[i][1] + (long long)H[i] * sts[i][2]))
+      return fail(DLLM_EUNSUPPORTED, "attention: per-sequence extent exceeds 32-bit element offsets");
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.out = out;
+  a.q_sb = q_strides[0]; a.q_st = (int)q_strides[1]; a.q_sh = (int)q_strides[2];
+  a.k_sb = k_strides[0]; a.k_st = (int)k_strides[1]; a.k_sh = (int)k_strides[2];
+  a.v_sb = v_strides[0]; a.v_st = (int)v_strides[1]; a.v_sh = (int)v_strides[2];
+  a.B = B; a.L = L; a.Hq = Hq; a.Hkv = Hkv; a.d = d; a.C = block;
+  a.leak = flags & 1;
+  a.scale_log2e = scale * 1.4426950408889634f;
+  const int esz = dtype == DT_BF16 ? 2 : 4;
+  const int vel = 16 / esz;
+  const int dw = d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : 256;
+  bool vec = (d == dw);
+  for (int i = 0; i < 3; ++i) vec = vec && (sts[i][0] % vel == 0) && (sts[i][1] % vel == 0) && (sts[i][2] % vel == 0);
+  vec = vec && ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0);
+  a.vec = vec;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16) {
+    switch (dw) {
+      case 32: return launch_attn<32, true>(a, st);
+      case 64: return launch_attn<64, true>(a, st);
+      case 128: return launch_attn<128, true>(a, st);
+      default: return launch_attn<256, true>(a, st);
+    }
+  }
+  if (dtype == DT_F32) {
+    switch (dw) {
+      case 32: return launch_attn<32, false>(a, st);
+      case 64: return launch_attn<64, false>(a, st);
+      case 128: return launch_attn<128, false>(a, st);
+      default: return launch_attn<256, false>(a, st);
+    }
+  }
+  return fail(DLLM_EUNSUPPORTED, "attention: dtype %d not supported", dtype);
+}

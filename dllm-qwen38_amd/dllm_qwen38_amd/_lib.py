@@ -44,7 +44,7 @@ _SIGNATURES = {
     "dllm_fork_layout": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "dllm_bd_attention_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
-        _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_int, _c_void_p]),
+        _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p]),
 }
 
 _LIB = None

@@ -1,0 +1,83 @@
+"""Complementary-mask block-diffusion attention on the MI355X HIP kernel.
+
+Replaces the FULL (attention) arm of the reference's `_layer_step` (src/dllm_qwen38/blockdiff.py:
+178-182): the reference builds an additive [1,1,2L,2L] mask (blockdiff.py:50-66) and runs HF's eager
+attention (transformers modeling_qwen3_5.py:604-626) over cat([x_t, x_0]). Here the visibility rule is
+evaluated from (L, block) inside the kernel; fully hidden tiles are never computed and no mask tensor
+exists. `complementary_mask` / `block_causal_mask` are still provided (dense, for the oracle and the
+mask-leak fault), as in the reference.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _neg(dtype: torch.dtype) -> float:
+    return torch.finfo(dtype).min
+
+
+def block_causal_mask(seq_len: int, block: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """[1, 1, S, S] additive mask: token i sees j iff block(j) <= block(i) (blockdiff.py:43-47)."""
+    idx = torch.arange(seq_len, device=device) // block
+    allowed = idx[None, :] <= idx[:, None]
+    return torch.zeros(seq_len, seq_len, dtype=dtype, device=device).masked_fill(~allowed, _neg(dtype))[None, None]
+
+
+def complementary_mask(seq_len: int, block: int, dtype: torch.dtype, device, *, leak_xt_prefix: bool = False):
+    """[1, 1, 2L, 2L] additive mask over cat([x_t, x_0]) (blockdiff.py:50-66); leak_xt_prefix=True is the
+    deliberately wrong mask (x_t block k also sees x_t blocks < k)."""
+    L = seq_len
+    idx = torch.arange(L, device=device) // block
+    bi, bj = idx[:, None], idx[None, :]
+    tt = (bj <= bi) if leak_xt_prefix else (bj == bi)
+    top = torch.cat([tt, bj < bi], 1)
+    bottom = torch.cat([torch.zeros(L, L, dtype=torch.bool, device=device), bj <= bi], 1)
+    allowed = torch.cat([top, bottom], 0)
+    return torch.zeros(2 * L, 2 * L, dtype=dtype, device=device).masked_fill(~allowed, _neg(dtype))[None, None]
+
+
+def bd_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int, scale: float | None = None,
+                 leak_xt_prefix: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention over cat([x_t, x_0]) under the complementary mask.
+
+    q [B, 2L, Hq, d], k/v [B, 2L, Hkv, d] (token-major, any batch/token/head strides, last dim
+    contiguous; rotary already applied) -> [B, 2L, Hq, d]. scale defaults to d^-1/2 ([hf]:638)."""
+    dev = _lib.require_device(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [B, 2L, H, d]")
+    B, S, Hq, d = q.shape
+    if S % 2:
+        raise ValueError(f"sequence {S} is not cat([x_t, x_0]) of two equal halves")
+    L = S // 2
+    if L % block:
+        raise ValueError(f"L={L} is not a multiple of block={block}")
+    if k.shape[:2] != (B, S) or v.shape != k.shape or k.shape[-1] != d:
+        raise ValueError("k and v must be [B, 2L, Hkv, d] matching q")
+    Hkv = k.shape[2]
+    if Hq % Hkv:
+        raise ValueError(f"query heads {Hq} not a multiple of key/value heads {Hkv}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k, v dtypes differ")
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    if out is None:
+        out = torch.empty(B, S, Hq, d, dtype=q.dtype, device=dev)
+    elif tuple(out.shape) != (B, S, Hq, d) or not out.is_contiguous() or out.dtype != q.dtype:
+        raise ValueError("out must be a contiguous [B, 2L, Hq, d] tensor of q's dtype")
+    sc = d ** -0.5 if scale is None else float(scale)
+    _lib.check(_lib.lib().dllm_bd_attention_fwd(
+        q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
+        out.data_ptr(), B, L, Hq, Hkv, d, block, sc, _lib.dtype_code(q.dtype), 1 if leak_xt_prefix else 0,
+        _lib.stream_handle(dev)), "dllm_bd_attention_fwd")
+    return out
+
+
+def attention_flops(B: int, L: int, Hq: int, d: int, block: int, leak: bool = False) -> int:
+    """Algorithmic flops over the visible (query, key) pairs only: 4*d per pair and query head."""
+    nb = L // block
+    sq = block * block
+    tt = sq * (nb * (nb + 1) // 2) if leak else sq * nb
+    pairs = tt + sq * (nb * (nb - 1) // 2) + sq * (nb * (nb + 1) // 2)
+    return B * Hq * pairs * 4 * d

@@ -108,6 +108,21 @@ int dllm_causal_conv1d_fwd(const void* x, const int64_t* x_strides, const void* 
 int dllm_fork_layout(int B, int L, int block, int width, int32_t* row, int32_t* state_src,
                      int32_t* prefix_pos, void* stream);
 
+/*
+ * Complementary-mask block-diffusion attention (flash style, hidden tiles skipped).
+ * Replaces the FULL arm of src/dllm_qwen38/blockdiff.py:178-182 with the [2L,2L] additive mask of
+ * blockdiff.py:50-66 (never materialised here) and [hf]:604-626 eager_attention_forward (GQA by
+ * indexing instead of repeat_kv). q [B,2L,Hq,d], k/v [B,2L,Hkv,d] (halves ordered
+ * cat([x_t, x_0]), rotary already applied), strides {b,t,h} in elements, last dim contiguous;
+ * out [B,2L,Hq,d] contiguous, same dtype. Visibility with blocks of `block` tokens per half:
+ * x_t->x_t same block, x_t->x_0 earlier blocks, x_0->x_0 block-causal, x_0->x_t never.
+ * flags bit 0: the "mask-leak" fault (x_t block k also sees x_t blocks < k, blockdiff.py:61).
+ * Scores and softmax in fp32; P rounded to the input dtype before P.V ([hf]:621-622); d <= 256.
+ */
+int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                          const void* v, const int64_t* v_strides, void* out, int B, int L, int Hq, int Hkv,
+                          int d, int block, float scale, int dtype, int flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,232 @@
+"""Block-diffusion two-stream forward of a Qwen3.5/3.8 hybrid on the MI355X HIP kernels.
+
+Drop-in for the reference's `src/dllm_qwen38/blockdiff.py`:
+  block_diffusion_forward (blockdiff.py:96-203), BreakMode (:69-88), complementary_mask /
+  block_causal_mask (:43-66), and LayerStep, the per-layer unit of the FSDP trainer
+  (fsdp_train.py:83-130), which here calls the same `layer_step` function as the stack driver so
+  the fork exists in one place.
+
+Visibility contract (x_t = noised stream, x_0 = clean stream, block(i) = i // block):
+x_t token i sees x_t token j iff block(j) == block(i); x_t sees x_0 iff block(j) < block(i);
+x_0 sees x_0 iff block(j) <= block(i); x_0 never sees x_t.
+
+Per layer:
+  * linear-attention (Gated DeltaNet) layers: one projection GEMM per weight over both streams,
+    then ONE fused fork op (`gdn.gdn_state_fork`): the short conv of both streams with the clean
+    3-token prefix carried into every noised block, and the clean recurrence whose state at every
+    block boundary seeds that block's noised recurrence on the fly (no state copy, no shifted
+    initial-state tensor, no prefix tensor), then the gated norm and out_proj over both streams;
+  * full-attention layers: projections, q/k RMSNorm and partial RoPE (positions 0..L-1 shared by
+    both halves), then the complementary-mask attention kernel, which derives visibility from
+    (L, block) and skips hidden tiles (no [2L, 2L] mask exists), then the sigmoid output gate and
+    o_proj.
+The GEMMs, norms, RoPE and gates run as torch ops on the same stream; the mixers are the HIP
+kernels of libdllm_hip.so. Forward only: the HIP ops have no backward, so a call that would need
+gradients raises instead of returning a graph that silently stops at the kernels.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import attention, gdn
+from .attention import block_causal_mask, complementary_mask  # noqa: F401  (re-exported, reference names)
+
+FULL = "full_attention"
+LINEAR = "linear_attention"
+
+
+@dataclass
+class BreakMode:
+    """Deliberate faults, each of which must make the equivalence check fail (blockdiff.py:69-88)."""
+
+    name: str = "none"
+
+    @property
+    def concat_causal_gdn(self) -> bool:
+        """GDN over cat([x_t, x_0]) as one causal sequence."""
+        return self.name == "concat-causal-gdn"
+
+    @property
+    def leak_xt_prefix(self) -> bool:
+        """x_t block k also sees x_t blocks < k in attention."""
+        return self.name == "mask-leak"
+
+    @property
+    def drop_conv_prefix(self) -> bool:
+        """The state is forked but the short conv starts cold at every noised block."""
+        return self.name == "no-conv-prefix"
+
+
+def _eps(norm) -> float:
+    return float(getattr(norm, "eps", getattr(norm, "variance_epsilon", 1e-6)))
+
+
+def rmsnorm(x: torch.Tensor, norm) -> torch.Tensor:
+    """Qwen3.5 RMSNorm: fp32 normalisation, weight applied as (1 + w), cast back ([hf]:720-737)."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + _eps(norm))
+    return (y * (1.0 + norm.weight.float())).type_as(x)
+
+
+def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, norm) -> torch.Tensor:
+    """rmsnorm(x) * w * silu(z): norm in fp32, weight product in x's dtype ([hf]:168-184)."""
+    dt = x.dtype
+    xf = x.float()
+    y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + _eps(norm))).to(dt)
+    return (norm.weight * y * F.silu(z.float())).to(dt)
+
+
+def mlp(m, x: torch.Tensor) -> torch.Tensor:
+    """SwiGLU ([hf]:704-717)."""
+    return m.down_proj(F.silu(m.gate_proj(x)) * m.up_proj(x))
+
+
+def rotary_tables(text_model, L: int, device, dtype):
+    """cos/sin [L, rotary_dim] for positions 0..L-1 in `dtype` (text-only rotary: the three mRoPE
+    position sections coincide, so the table is the plain one; [hf]:84-166, blockdiff.py:91-93)."""
+    inv = text_model.rotary_emb.inv_freq.to(device=device, dtype=torch.float32)
+    fr = torch.arange(L, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+    emb = torch.cat([fr, fr], -1)
+    scale = float(getattr(text_model.rotary_emb, "attention_scaling", 1.0))
+    return (emb.cos() * scale).to(dtype), (emb.sin() * scale).to(dtype)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Partial RoPE on the first rotary_dim dims of x [B, S, H, d] with tables [S, rotary_dim]
+    ([hf]:554-589)."""
+    rd = cos.shape[-1]
+    xr, xp = x[..., :rd], x[..., rd:]
+    c, s = cos[:, None, :], sin[:, None, :]
+    half = rd // 2
+    rot = torch.cat([-xr[..., half:], xr[..., :half]], -1)
+    return torch.cat([xr * c + rot * s, xp], -1)
+
+
+def _gdn_fork_arm(m, n0: torch.Tensor, nt: torch.Tensor, block: int, fault: BreakMode):
+    """LINEAR arm of the layer (blockdiff.py:153-177): both streams through one fused fork op."""
+    B, L, _ = n0.shape
+    if fault.concat_causal_gdn:
+        out, _, _ = gdn.gdn_mixer_forward(m, torch.cat([nt, n0], 1), chunk_size=block, need_states=False)
+        return out[:, L:], out[:, :L]
+    x = torch.cat([nt, n0], 0)  # [2B, L, D]: rows 0..B-1 noised, B..2B-1 clean
+    raw = m.in_proj_qkv(x)
+    z = m.in_proj_z(x)
+    beta, g = gdn._beta_g(m, m.in_proj_b(x), m.in_proj_a(x))
+    Hv, Dv = m.num_v_heads, m.head_v_dim
+    core = torch.empty(2 * B, L, Hv, Dv, dtype=raw.dtype, device=raw.device)
+    gdn.gdn_state_fork(raw[B:], raw[:B], m.conv1d.weight.squeeze(1), beta[B:], beta[:B], g[B:], g[:B],
+                       num_k_heads=m.num_k_heads, num_v_heads=Hv, head_k_dim=m.head_k_dim, head_v_dim=Dv,
+                       block=block, conv_bias=m.conv1d.bias, need_states=False, need_tails=False,
+                       fault="no-conv-prefix" if fault.drop_conv_prefix else None,
+                       out={"ot": core[:B], "o0": core[B:]})
+    o = gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm).reshape(2 * B, L, -1)
+    out = m.out_proj(o)
+    return out[B:], out[:B]
+
+
+def _attention_arm(att, n0: torch.Tensor, nt: torch.Tensor, cos, sin, block: int, fault: BreakMode):
+    """FULL arm (blockdiff.py:178-182 through [hf]:656-701) on cat([x_t, x_0])."""
+    B, L, _ = n0.shape
+    x = torch.cat([nt, n0], 1)  # [B, 2L, D]
+    S = 2 * L
+    hd = att.head_dim
+    q, gate = torch.chunk(att.q_proj(x).view(B, S, -1, 2 * hd), 2, dim=-1)
+    gate = gate.reshape(B, S, -1)
+    q = rmsnorm(q, att.q_norm)
+    k = rmsnorm(att.k_proj(x).view(B, S, -1, hd), att.k_norm)
+    v = att.v_proj(x).view(B, S, -1, hd)
+    q = apply_rope(q, cos, sin)
+    k = apply_rope(k, cos, sin)
+    o = attention.bd_attention(q, k, v, block=block, scale=float(att.scaling), leak_xt_prefix=fault.leak_xt_prefix)
+    out = att.o_proj(o.reshape(B, S, -1) * torch.sigmoid(gate))
+    return out[:, L:], out[:, :L]
+
+
+def layer_step(layer, kind: str, h0: torch.Tensor, ht: torch.Tensor, *, block: int, cos2, sin2,
+               fault: BreakMode | None = None):
+    """One decoder layer for both streams (blockdiff.py:147-188). cos2/sin2: rotary tables
+    [2L, rotary_dim] for cat([x_t, x_0]) (positions shared by the halves)."""
+    fault = fault or BreakMode()
+    n0, nt = rmsnorm(h0, layer.input_layernorm), rmsnorm(ht, layer.input_layernorm)
+    if kind == LINEAR:
+        o0, ot = _gdn_fork_arm(layer.linear_attn, n0, nt, block, fault)
+    elif kind == FULL:
+        o0, ot = _attention_arm(layer.self_attn, n0, nt, cos2, sin2, block, fault)
+    else:
+        raise ValueError(f"unknown layer type {kind}")
+    h0, ht = h0 + o0, ht + ot
+    h0 = h0 + mlp(layer.mlp, rmsnorm(h0, layer.post_attention_layernorm))
+    ht = ht + mlp(layer.mlp, rmsnorm(ht, layer.post_attention_layernorm))
+    return h0, ht
+
+
+def _forbid_grad(*modules):
+    if torch.is_grad_enabled() and any(p.requires_grad for mod in modules for p in mod.parameters()):
+        raise RuntimeError(
+            "block_diffusion_forward runs forward-only HIP kernels (no backward is built); call it under "
+            "torch.no_grad() / torch.inference_mode() or freeze the parameters")
+
+
+def block_diffusion_forward(text_model, lm_head, x0_ids: torch.Tensor, xt_ids: torch.Tensor, block: int, *,
+                            fault: BreakMode | None = None, layers: int | None = None, output: str = "logits",
+                            checkpointing: bool = False):
+    """Two-stream forward (blockdiff.py:96-203). Returns (logits_t [B, L, V], logits_0 [B, L, V]) or,
+    with output="hidden", the final-normed hidden states [B, L, D] of both streams.
+
+    x0_ids / xt_ids: [B, L] with L a multiple of `block` (ValueError otherwise). `layers` truncates
+    the stack. `checkpointing` is accepted for signature compatibility; there is nothing to
+    checkpoint in a forward-only pass."""
+    fault = fault or BreakMode()
+    if output not in ("logits", "hidden"):
+        raise ValueError(f"output must be 'logits' or 'hidden', got {output!r}")
+    cfg = text_model.config
+    if x0_ids.shape != xt_ids.shape or x0_ids.ndim != 2:
+        raise ValueError("x0_ids and xt_ids must both be [B, L]")
+    B, L = x0_ids.shape
+    if L % block:
+        raise ValueError(f"L={L} is not a multiple of block={block}")
+    _forbid_grad(text_model, lm_head)
+    del checkpointing
+
+    h0 = text_model.embed_tokens(x0_ids)
+    ht = text_model.embed_tokens(xt_ids)
+    cos, sin = rotary_tables(text_model, L, h0.device, h0.dtype)
+    cos2, sin2 = torch.cat([cos, cos], 0), torch.cat([sin, sin], 0)
+    n = cfg.num_hidden_layers if layers is None else layers
+    for i in range(n):
+        h0, ht = layer_step(text_model.layers[i], cfg.layer_types[i], h0, ht, block=block, cos2=cos2, sin2=sin2,
+                            fault=fault)
+    ht, h0 = rmsnorm(ht, text_model.norm), rmsnorm(h0, text_model.norm)
+    if output == "hidden":
+        return ht, h0
+    return lm_head(ht), lm_head(h0)
+
+
+class LayerStep(nn.Module):
+    """One decoder layer for both streams as a module (fsdp_train.py:83-130).
+
+    forward(h0, ht, pos, mask, block): pos = (cos, sin) rotary tables for cat([x_t, x_0]), shaped
+    [..., 2L, rotary_dim] (leading dims broadcast; HF's rotary output is accepted). The attention
+    kernel derives visibility from `block`, so `mask` must be None: a dense mask is refused rather
+    than ignored (select the leak fault with `fault=BreakMode("mask-leak")`)."""
+
+    def __init__(self, layer, kind: str, fault: BreakMode | None = None):
+        super().__init__()
+        self.layer = layer
+        self.kind = kind
+        self.fault = fault or BreakMode()
+
+    def forward(self, h0, ht, pos, mask, block: int):
+        if mask is not None:
+            raise ValueError("LayerStep takes no dense attention mask: visibility is derived from block")
+        _forbid_grad(self.layer)
+        cos, sin = pos
+        S = 2 * h0.shape[1]
+        cos2 = cos.reshape(-1, S, cos.shape[-1])[0].to(h0.dtype)
+        sin2 = sin.reshape(-1, S, sin.shape[-1])[0].to(h0.dtype)
+        return layer_step(self.layer, self.kind, h0, ht, block=block, cos2=cos2, sin2=sin2, fault=self.fault)

@@ -3,46 +3,15 @@
 import pytest
 import torch
 
+from _tiny import noised_ids, tiny_hf_model
 from oracle import model_ref
 
 FAULTS = ("concat-causal-gdn", "mask-leak", "no-conv-prefix")
 
 
-def tiny_hf_model(seed=0, layers=8, vocab=256):
-    """A random Qwen3.5 text model of the reference's tiny test size (hidden 64, 6 GDN + 2 attention
-    layers, heads 4/2 of dim 16, GDN heads 2 key / 4 value of dim 16, conv width 4)."""
-    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
-    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextModel
-
-    torch.manual_seed(seed)
-    cfg = Qwen3_5TextConfig(
-        vocab_size=vocab, hidden_size=64, intermediate_size=128, num_hidden_layers=layers,
-        num_attention_heads=4, num_key_value_heads=2, head_dim=16, linear_num_key_heads=2,
-        linear_num_value_heads=4, linear_key_head_dim=16, linear_value_head_dim=16, linear_conv_kernel_dim=4,
-        max_position_embeddings=4096,
-        rope_parameters={"rope_theta": 10000.0, "mrope_section": [2, 1, 1], "partial_rotary_factor": 0.25},
-        attn_implementation="eager")
-    model = Qwen3_5TextModel(cfg).eval()
-    # non-trivial norm weights and gates so that every weight path is exercised
-    with torch.no_grad():
-        for n, p in model.named_parameters():
-            if n.endswith("norm.weight"):
-                p.normal_(0.0, 0.1)
-    lm_head = torch.nn.Linear(64, vocab, bias=False)
-    return model, lm_head
-
-
 @pytest.fixture(scope="module")
 def tiny():
     return tiny_hf_model(seed=0)
-
-
-def _ids(B, L, vocab=256, seed=1):
-    g = torch.Generator().manual_seed(seed)
-    x0 = torch.randint(0, vocab, (B, L), generator=g)
-    xt = x0.clone()
-    xt[torch.rand(B, L, generator=g) < 0.5] = vocab - 1
-    return x0, xt
 
 
 def test_norms_and_mlp_match_transformers(tiny):
@@ -109,7 +78,7 @@ def test_fork_forward_equals_per_block_oracle_and_faults_are_detected(tiny):
     of cat(x_0 prefix, x_t block); the clean stream equals the block-causal forward of x_0; every
     deliberate fault breaks the noised stream."""
     model, lm_head = tiny
-    x0, xt = _ids(2, 32, seed=6)
+    x0, xt = noised_ids(2, 32, seed=6)
     lt, l0 = model_ref.block_diffusion_forward(model, lm_head, x0, xt, 8)
     ref_t = model_ref.reference_block_logits(model, lm_head, x0, xt, 8)
     ref_0 = model_ref.reference_clean_logits(model, lm_head, x0, 8)

@@ -47,6 +47,12 @@ template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf
 // Round an fp32 value through type T (identity for float).
 template <typename T> __device__ __forceinline__ float round_through(float x) { return to_f32(from_f32<T>(x)); }
 
+// SiLU x * sigmoid(x) from the hardware base-2 exponential and reciprocal (each within 1 ulp):
+// within a few fp32 ulp of x / (1 + e^-x); large negative x gives -0 where the exact value underflows.
+__device__ __forceinline__ float silu_f32(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
 // Fragment: 16 rho-ordered operand values for one 32-wide K slice.
 template <bool BF16> struct Frag;
 template <> struct Frag<true> { bf16x8 lo, hi; };     // values 0..7 and 8..15
@@ -77,6 +83,23 @@ __device__ __forceinline__ void lds_frag(const float* base, int h, Frag<false>& 
     const f32x4 r = *(const f32x4*)(base + 8 * m + 4 * h);
     f.v[4 * m + 0] = r[0]; f.v[4 * m + 1] = r[1]; f.v[4 * m + 2] = r[2]; f.v[4 * m + 3] = r[3];
   }
+}
+
+// Fragment of the TRANSPOSED access to a row-major bf16 buffer: lane (l32, h) gets column
+// col0 + l32 at rows (k) 8m + 4h + e, e = 0..3 (rho order), where base points at (row 0, col0).
+// Uses the gfx950 LDS transpose read: in each group of 16 lanes, source lane s supplies the
+// address of 4 consecutive columns (4 (s & 3) onwards) of row (s >> 2), and result lane i receives
+// column i of those 4 rows. Row stride and col0 must keep every address 8-byte aligned.
+__device__ __forceinline__ void lds_frag_tr(const bf16* base, int row_stride, int lane, Frag<true>& f) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  const int s = lane & 15;
+  const bf16* p = base + (4 * (lane >> 5) + (s >> 2)) * row_stride + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  bf16x4 r[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    r[m] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 8 * m * row_stride));
+  f.lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+  f.hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // acc += A_frag * B_frag over one 32-wide K slice.

@@ -13,7 +13,8 @@
 //
 // Arithmetic follows the reference cast points: the input is converted to the weight's dtype, the
 // K products are accumulated in fp32, the sum is rounded to the weight dtype, SiLU is evaluated in
-// fp32 and rounded to the weight dtype, and the result is returned in the input dtype.
+// fp32 (hardware exp2 and reciprocal) and rounded to the weight dtype, and the result is returned
+// in the input dtype.
 #include "common.h"
 
 namespace dllm {
@@ -90,8 +91,8 @@ __global__ __launch_bounds__(256) void conv_fork_kernel(
       at = __builtin_fmaf(wv[e][K - 1], ctv, at);
       a0 = round_through<TW>(a0);
       at = round_through<TW>(at);
-      o0[e] = from_f32<TX>(round_through<TW>(a0 / (1.0f + expf(-a0))));
-      ot[e] = from_f32<TX>(round_through<TW>(at / (1.0f + expf(-at))));
+      o0[e] = from_f32<TX>(round_through<TW>(silu_f32(a0)));
+      ot[e] = from_f32<TX>(round_through<TW>(silu_f32(at)));
 #pragma unroll
       for (int j = 0; j < K - 2; ++j) { h0[j][e] = h0[j + 1][e]; ht[j][e] = ht[j + 1][e]; }
       h0[K - 2][e] = c0v;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(256) void conv_generic_kernel(
     float a = bv;
     for (int j = 0; j < K; ++j) a = __builtin_fmaf(wv[j], at(t - (K - 1) + j), a);
     a = round_through<TW>(a);
-    if (silu) a = round_through<TW>(a / (1.0f + expf(-a)));
+    if (silu) a = round_through<TW>(silu_f32(a));
     y[((long long)b * T + t) * C + c] = from_f32<TX>(a);
   }
 }

@@ -95,6 +95,11 @@ struct GdnSmem {
   static constexpr int O_YF = O_TF + 32 * FROW * 4;
   static constexpr int O_VEC = O_YF + 16 * 20 * 4;  // eight per-row vectors of 32 floats
   static constexpr int STREAM_BYTES = ((O_VEC + 8 * 32 * 4) + 15) & ~15;
+  // bf16 keeps k and v row-major (transposed operands come from LDS transpose reads): the two
+  // transposed regions hold W rows [32][QROW] and v rows [32][VROW] instead
+  static constexpr int VROW = DVW + 8;
+  static_assert(!BF16 || 32 * QROW <= DK * TROW, "W rows must fit the k-transpose region");
+  static_assert(!BF16 || 32 * VROW <= DVW * TROW, "v rows must fit the v-transpose region");
   static constexpr int FRAG_BYTES = 16 * (int)sizeof(OpT);
   // state operand fragments published by the clean set for the noised set: [NSL][KT][64 lanes]
   static constexpr int O_SB = NS * STREAM_BYTES;
@@ -172,8 +177,11 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
   unsigned char* sbase = smem + set * SM::STREAM_BYTES;
   OpT* const QH = (OpT*)(sbase + SM::O_QH);    // raw q rows            [32][DK]
   OpT* const KH = (OpT*)(sbase + SM::O_KH);    // raw k rows, then W    [32][DK]
-  OpT* const KTr = (OpT*)(sbase + SM::O_KT);   // raw k transposed      [DK][32]
-  OpT* const VT = (OpT*)(sbase + SM::O_VT);    // raw v transposed      [DVW][32]
+  OpT* const KTr = (OpT*)(sbase + SM::O_KT);   // fp32: raw k transposed [DK][32]
+  OpT* const VT = (OpT*)(sbase + SM::O_VT);    // fp32: raw v transposed [DVW][32]
+  OpT* const WH = KTr;                         // bf16: W rows           [32][QROW]
+  OpT* const VH = VT;                          // bf16: raw v rows       [32][VROW]
+  constexpr int VROW = SM::VROW;
   OpT* const PP = (OpT*)(sbase + SM::O_P);     // P with q row norms    [32][32]
   OpT* const T1 = (OpT*)(sbase + SM::O_T1);    // T diag(beta e^g rnk)  [32][32]
   OpT* const T2 = (OpT*)(sbase + SM::O_T2);    // T diag(beta)          [32][32]
@@ -288,15 +296,28 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         *(V16*)(QH + lr * QROW + qe0) = xq[0];
         *(V16*)(KH + lr * QROW + qe0) = xk[0];
       }
+      if constexpr (BF16) {  // v rows as loaded: the transposed operands come from transpose reads
+        if constexpr (TWO_V) {
+          constexpr int HVV = NV / 2 / EPV;
 #pragma unroll
-      for (int i = 0; i < NE / 2; ++i) {
-        KTr[(qe0 + i) * TROW + lr] = xk[i / EPV][i % EPV];
-        KTr[(qe1 + i) * TROW + lr] = xk[(NE / 2 + i) / EPV][(NE / 2 + i) % EPV];
-      }
+          for (int i = 0; i < HVV; ++i) {
+            *(V16*)(VH + lr * VROW + ve0 + i * EPV) = xv[i];
+            *(V16*)(VH + lr * VROW + ve1 + i * EPV) = xv[HVV + i];
+          }
+        } else {
+          *(V16*)(VH + lr * VROW + ve0) = xv[0];
+        }
+      } else {
 #pragma unroll
-      for (int i = 0; i < NV / 2; ++i) {
-        VT[(ve0 + i) * TROW + lr] = xv[i / EPV][i % EPV];
-        VT[(ve1 + i) * TROW + lr] = xv[(NV / 2 + i) / EPV][(NV / 2 + i) % EPV];
+        for (int i = 0; i < NE / 2; ++i) {
+          KTr[(qe0 + i) * TROW + lr] = xk[i / EPV][i % EPV];
+          KTr[(qe1 + i) * TROW + lr] = xk[(NE / 2 + i) / EPV][(NE / 2 + i) % EPV];
+        }
+#pragma unroll
+        for (int i = 0; i < NV / 2; ++i) {
+          VT[(ve0 + i) * TROW + lr] = xv[i / EPV][i % EPV];
+          VT[(ve1 + i) * TROW + lr] = xv[(NV / 2 + i) / EPV][(NV / 2 + i) % EPV];
+        }
       }
       // q row norm (the k norms come from the diagonal of K K^T)
       float ss = 0.f;
@@ -352,20 +373,29 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
       const bool isG = (u == (set == 0 ? 0 : 1));
       const bool isQK = (u == (set == 0 ? 2 : 3));
       if (isG || isQK) {
-        const OpT* X = isG ? KH : QH;
-        F fa[KT], fb[KT];
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-          lds_frag(X + l32 * QROW + kt * 32, h, fa[kt]);
-          lds_frag(KH + l32 * QROW + kt * 32, h, fb[kt]);
-        }
-        f32x4 gam4[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(GAML + 8 * m + 4 * h);
-        const float gj = GAML[l32];
         f32x16 acc = zero16();
+        f32x4 gam4[4];
+        if (isG) {  // K K^T: one operand read serves both sides
+          F fa[KT];
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fb[kt]);
+          for (int kt = 0; kt < KT; ++kt) lds_frag(KH + l32 * QROW + kt * 32, h, fa[kt]);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(GAML + 8 * m + 4 * h);
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fa[kt]);
+        } else {
+          F fa[KT], fb[KT];
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) {
+            lds_frag(QH + l32 * QROW + kt * 32, h, fa[kt]);
+            lds_frag(KH + l32 * QROW + kt * 32, h, fb[kt]);
+          }
+#pragma unroll
+          for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(GAML + 8 * m + 4 * h);
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fb[kt]);
+        }
+        const float gj = GAML[l32];
         if (isG) {
           // k norms from the diagonal of K K^T: lane (j, h = (j>>2)&1) holds element (j, j)
           float dg = 0.f;
@@ -532,11 +562,17 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
       const int kt = u;
       F fa, fb;
       lds_frag(T1 + l32 * TROW, h, fa);
-      lds_frag(KTr + (kt * 32 + l32) * TROW, h, fb);
+      if constexpr (BF16) {
+        lds_frag_tr(KH + kt * 32, QROW, lane, fb);
+      } else {
+        lds_frag(KTr + (kt * 32 + l32) * TROW, h, fb);
+      }
       f32x16 acc = zero16();
       mma32(acc, fa, fb);
+      // bf16: W gets its own rows (raw k stays for the state update); fp32: raw k is dead
+      OpT* const Wd = BF16 ? WH : KH;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) KH[rho(v, h) * QROW + kt * 32 + l32] = from_f32<OpT>(acc[v]);  // raw k is dead
+      for (int v = 0; v < 16; ++v) Wd[rho(v, h) * QROW + kt * 32 + l32] = from_f32<OpT>(acc[v]);
     }
     __syncthreads();
 
@@ -546,7 +582,11 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
       {
         F fa, fb;
         lds_frag(T2 + l32 * TROW, h, fa);
-        lds_frag(VT + (u * 32 + l32) * TROW, h, fb);
+        if constexpr (BF16) {
+          lds_frag_tr(VH + u * 32, VROW, lane, fb);
+        } else {
+          lds_frag(VT + (u * 32 + l32) * TROW, h, fb);
+        }
         mma32(accU, fa, fb);
       }
       constexpr int KH2 = KT >= 2 ? KT / 2 : 1;  // fragment reads in batches of KH2 K-slices
@@ -555,7 +595,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         F fw[KH2], fq[KH2], sx[KH2];
 #pragma unroll
         for (int q = 0; q < KH2; ++q) {
-          lds_frag(KH + l32 * QROW + (k0 + q) * 32, h, fw[q]);
+          lds_frag((BF16 ? WH : KH) + l32 * QROW + (k0 + q) * 32, h, fw[q]);
           lds_frag(QH + l32 * QROW + (k0 + q) * 32, h, fq[q]);
           if constexpr (FORK) {
             sx[q] = *SBUF(u, k0 + q);
@@ -619,7 +659,13 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         acc_to_frag(vd, fd);
         F fk[KT];
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt) lds_frag(KTr + (kt * 32 + l32) * TROW, h, fk[kt]);
+        for (int kt = 0; kt < KT; ++kt) {
+          if constexpr (BF16) {
+            lds_frag_tr(KH + kt * 32, QROW, lane, fk[kt]);
+          } else {
+            lds_frag(KTr + (kt * 32 + l32) * TROW, h, fk[kt]);
+          }
+        }
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll

@@ -265,6 +265,10 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
     }
   };
   issue_loads(0);
+  // The waits below keep loads and stores from being in flight together at the points where the
+  // prefetched registers are read: with both kinds pending the compiler must wait for every
+  // outstanding store (vmcnt(0)) before using a loaded value.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): nothing in flight at the loop head
   const V16 vzero = {};
 
   for (int c = 0; c < ntiles; ++c) {
@@ -629,6 +633,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         lds_frag(PP + l32 * TROW, h, fp);
         mma32(accQS, fp, fv);
       }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile's prefetch has landed
       // output rows of the real tokens: uniform row bases, one 32-bit lane offset
       {
         const int rs = opaque(a.Hv * a.Dv);  // token stride of out
@@ -666,24 +671,28 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
             lds_frag(KTr + (kt * 32 + l32) * TROW, h, fk[kt]);
           }
         }
+        // state snapshot after every snap_every tiles; for a full head (compile-time row stride)
+        // each K slice is stored as soon as its update is issued
+        const bool snap = a.states && ((c + 1) % a.snap_every) == 0;
+        const int dv = opaque(a.Dv);
+        const bool snap_fast = snap && a.Dk == DK && dv == DVW;
+        float* const sb = snap ? a.states + (((long long)b * nsnap + ((c + 1) / a.snap_every - 1)) * a.Hv + hv) *
+                                                (long long)a.Dk * a.Dv + scol0
+                               : nullptr;
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) S[kt][v] *= lam;
           mma32(S[kt], fk[kt], fd);
-        }
-        if (a.states && ((c + 1) % a.snap_every) == 0) {
-          const int sn = (c + 1) / a.snap_every - 1;
-          float* sb = a.states + (((long long)b * nsnap + sn) * a.Hv + hv) * (long long)a.Dk * a.Dv + scol0;
-          const int dv = opaque(a.Dv);
-          if (a.Dk == DK && dv == DVW) {  // full head: compile-time row stride, immediate offsets
+          if (snap_fast) {
             float* lp = sb + 4 * h * DVW + l32;
 #pragma unroll
-            for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-              for (int v = 0; v < 16; ++v)
-                __builtin_nontemporal_store(S[kt][v], lp + (32 * kt + ((v >> 2) << 3) + (v & 3)) * DVW);
-          } else if (col_ok) {
+            for (int v = 0; v < 16; ++v)
+              __builtin_nontemporal_store(S[kt][v], lp + (32 * kt + ((v >> 2) << 3) + (v & 3)) * DVW);
+          }
+        }
+        if (snap && !snap_fast) {
+          if (col_ok) {
             const unsigned lo = (unsigned)(4 * h * dv + l32);
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt)

@@ -15,8 +15,10 @@
 // Per wave and key tile: S^T = K Q^T on MFMA (rows = keys, lane = query), online softmax in fp32
 // with exp2, P rounded to the input dtype, then O^T += V^T P^T on MFMA: the accumulator layout of
 // S^T is directly the B-operand layout of P^T, and each lane owns one query column of O^T, so the
-// softmax rescale is a per-lane scalar. K tiles are staged row-major and V tiles transposed in a
-// double-buffered LDS ring, the next tile's global loads travelling during the current compute.
+// softmax rescale is a per-lane scalar (applied lazily, only when a running maximum grows by more
+// than 2^8). K and V tiles are staged row-major in a double-buffered LDS ring (bf16 V^T operands
+// come from gfx950 LDS transpose reads), the next tile's global loads travelling during the current
+// compute.
 // GQA: query head h reads KV head h / (Hq / Hkv), no repeat_kv copy.
 #include <type_traits>
 
@@ -70,9 +72,10 @@ template <int D, bool BF16>
 struct AttnSmem {
   using OpT = typename std::conditional<BF16, bf16, float>::type;
   static constexpr int KROW = D + (BF16 ? 8 : 4);  // K tile [32][D]
-  static constexpr int VROW = 36;                    // V^T tile [D][32]
+  // bf16: V tile row-major [32][D] (V^T operands come from LDS transpose reads); fp32: V^T [D][32]
+  static constexpr int VROW = BF16 ? D + 8 : 36;
   static constexpr int K_BYTES = 32 * KROW * (int)sizeof(OpT);
-  static constexpr int V_BYTES = D * VROW * (int)sizeof(OpT);
+  static constexpr int V_BYTES = (BF16 ? 32 : D) * VROW * (int)sizeof(OpT);
   static constexpr int STAGE = K_BYTES + V_BYTES;
   static constexpr int TOTAL = 2 * STAGE;
 };
@@ -212,8 +215,12 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
       const V16 kx = ok ? rk[q] : vz;
       const V16 vx = ok ? rv[q] : vz;
       *(V16*)(Ks + kr * KROW + e0) = kx;
+      if constexpr (BF16) {
+        *(V16*)(Vs + kr * VROW + e0) = vx;
+      } else {
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) Vs[(e0 + e) * VROW + kr] = vx[e];
+        for (int e = 0; e < EPV; ++e) Vs[(e0 + e) * VROW + kr] = vx[e];
+      }
     }
   };
 
@@ -265,18 +272,30 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int v = 1; v < 16; ++v) mx = fmaxf(mx, st[v]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(mrow, mx);
-      const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+      // Lazy rescale: the reference maximum moves only when some lane's tile maximum exceeds it by
+      // more than RESCALE_LOG2 (then O and l are rescaled, wave-uniformly); otherwise the
+      // unnormalised probabilities stay below 2^RESCALE_LOG2 and O, l keep accumulating against the
+      // same reference. O / l is unchanged; most tiles skip the O rescale entirely.
+      constexpr float RESCALE_LOG2 = 8.f;
+      if (__builtin_amdgcn_ballot_w64(mx > mrow + RESCALE_LOG2) != 0) {
+        const float mnew = fmaxf(mrow, mx);
+        const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) O[t][v] *= alpha;
+        lrow *= alpha;
+        mrow = mnew;
+      }
       float ps = 0.f;
       f32x16 p;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        p[v] = __builtin_amdgcn_exp2f(st[v] - mnew);
+        p[v] = __builtin_amdgcn_exp2f(st[v] - mrow);
         ps += p[v];
       }
       ps += __shfl_xor(ps, 32);
-      lrow = lrow * alpha + ps;
-      mrow = mnew;
+      lrow += ps;
       F pf;
       acc_to_frag(p, pf);
       // O^T += V^T P^T
@@ -285,13 +304,15 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
       for (int t0 = 0; t0 < DT; t0 += VB) {
         F vf[VB];
 #pragma unroll
-        for (int t = 0; t < VB; ++t) lds_frag(Vs + (32 * (t0 + t) + l32) * VROW, h, vf[t]);
-#pragma unroll
         for (int t = 0; t < VB; ++t) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) O[t0 + t][v] *= alpha;
-          mma32(O[t0 + t], vf[t], pf);
+          if constexpr (BF16) {
+            lds_frag_tr(Vs + 32 * (t0 + t), VROW, lane, vf[t]);
+          } else {
+            lds_frag(Vs + (32 * (t0 + t) + l32) * VROW, h, vf[t]);
+          }
         }
+#pragma unroll
+        for (int t = 0; t < VB; ++t) mma32(O[t0 + t], vf[t], pf);
       }
     }
     if (n + 1 < ntiles) store_tile(n + 1, (n + 1) & 1);

@@ -64,6 +64,12 @@ __device__ __forceinline__ int opaque(int x) {
   asm volatile("" : "+s"(x));
   return x;
 }
+// The same for a per-lane value: comparisons against it are evaluated where they are used instead
+// of being hoisted out of the tile loop as lane masks held in (spilled) scalar registers.
+__device__ __forceinline__ int opaque_v(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 // Sum over each aligned group of 8 lanes, returned to all 8 (DPP: no LDS round trip). The three
 // steps are quad_perm [1,0,3,2], quad_perm [2,3,0,1] and row_half_mirror.
@@ -273,6 +279,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
 
   for (int c = 0; c < ntiles; ++c) {
     const int t0 = c * a.sub;
+    const int lo = opaque_v(l32), ho = opaque_v(h);  // lane indices for masks (see opaque_v)
     __syncthreads();  // the previous tile's state phase is done with every LDS operand
 
     // ------------------------------------------------------------------ load phase (registers -> LDS)
@@ -342,7 +349,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
           const f32x4 g4 = *(const f32x4*)(GAML + q);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            if (q + e <= l32) gam += g4[e];
+            if (q + e <= lo) gam += g4[e];
             gall += g4[e];
           }
         }
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
           // k norms from the diagonal of K K^T: lane (j, h = (j>>2)&1) holds element (j, j)
           float dg = 0.f;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) dg = (rho(v, h) == l32) ? acc[v] : dg;
+          for (int v = 0; v < 16; ++v) dg = (rho(v, ho) == lo) ? acc[v] : dg;
           if (h == ((l32 >> 2) & 1)) RNK[l32] = a.l2norm ? rsqrtf(dg + 1e-6f) : 1.f;
           wave_lds_sync();
           f32x4 bet4[4], rnk4[4];
@@ -422,14 +429,14 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
               const int i = 8 * m + 4 * h + e;
               const float val = (bet4[m][e] * rnk4[m][e] * rj) * acc[4 * m + e] *
                                 __builtin_amdgcn_exp2f(gam4[m][e] - gj);
-              AF[i * FROW + l32] = (l32 < i) ? val : 0.f;
+              AF[i * FROW + l32] = (lo < 8 * m + 4 * ho + e) ? val : 0.f;
             }
           if (h == 0) EGLK[l32] = eglj * rj;
           wave_lds_sync();
           // level 0: four 8x8 diagonal blocks, one column per lane (lanes 0..31); lanes of odd
           // blocks also clear the block above (read as zero by level 2)
           if (h == 0) {
-            const int bb = l32 >> 3, cc = l32 & 7, o = 8 * bb;
+            const int bb = l32 >> 3, cc = lo & 7, o = 8 * bb;
             f32x4 ar[8][2];
 #pragma unroll
             for (int i = 1; i < 8; ++i) {
@@ -502,7 +509,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
             for (int e = 0; e < 4; ++e) {
               const int i = 8 * m + 4 * h + e;
               const float val = rnq4[m][e] * acc[4 * m + e] * __builtin_amdgcn_exp2f(gam4[m][e] - gj);
-              PP[i * TROW + l32] = from_f32<OpT>((l32 <= i) ? val : 0.f);
+              PP[i * TROW + l32] = from_f32<OpT>((lo <= 8 * m + 4 * ho + e) ? val : 0.f);
             }
           if (h == 0) EGQ[l32] = egj * rqj;
         }
@@ -514,7 +521,8 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
     // T[16:32][0:16] = -T16_1 (A[16:32][0:16] T16_0); the final entries elsewhere are already in TF.
     // Thread ts owns entry (ii, jj) of the 16x16 block and writes the scaled operand copies
     // T1 = T diag(beta e^gamma / ||k||) and T2 = T diag(beta) for four entries.
-    const int ii = ts >> 4, jj = ts & 15;
+    const int tso = opaque_v(ts);
+    const int ii = tso >> 4, jj = tso & 15;
     {
       f32x4 arow[4];
       float tcol[16];
@@ -523,8 +531,8 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
 #pragma unroll
       for (int kk = 0; kk < 16; ++kk) tcol[kk] = TF[kk * FROW + jj];
       // rows 0..15 (all columns) and the T16_1 block are final: scaled copies now
-      const int i0 = ts >> 4, j0 = (ts & 15) * 2;  // rows 0..15, columns j0, j0+1
-      const int i1 = 16 + (ts >> 4), j1 = 16 + (ts & 15);  // T16_1 block
+      const int i0 = tso >> 4, j0 = (tso & 15) * 2;  // rows 0..15, columns j0, j0+1
+      const int i1 = 16 + (tso >> 4), j1 = 16 + (tso & 15);  // T16_1 block
       const f32x2 t0v = *(const f32x2*)(TF + i0 * FROW + j0);
       const float t1v = TF[i1 * FROW + j1];
       const f32x2 b0 = *(const f32x2*)(BET + j0), e0 = *(const f32x2*)(EG + j0), r0 = *(const f32x2*)(RNK + j0);

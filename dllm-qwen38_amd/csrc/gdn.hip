@@ -394,6 +394,9 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
           for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(GAML + 8 * m + 4 * h);
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fa[kt]);
+          // issue every operand read before the MFMA chain (one LDS round trip, not one per slice)
+          __builtin_amdgcn_sched_group_barrier(0x100, 2 * KT + 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2 * KT, 0);
         } else {
           F fa[KT], fb[KT];
 #pragma unroll
@@ -405,6 +408,8 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
           for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(GAML + 8 * m + 4 * h);
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fb[kt]);
+          __builtin_amdgcn_sched_group_barrier(0x100, 4 * KT + 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2 * KT, 0);
         }
         const float gj = GAML[l32];
         if (isG) {

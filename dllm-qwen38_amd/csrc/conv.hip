@@ -68,38 +68,51 @@ __global__ __launch_bounds__(256) void conv_fork_kernel(
     }
   }
 
-  for (int r = 0; r < block; ++r) {
-    const long long off = row_base + (long long)(kblk * block + r) * Cd + c0;
-    const VecN<TX, VEC> x0v = *(const VecN<TX, VEC>*)(raw0 + off);
-    const VecN<TX, VEC> xtv = *(const VecN<TX, VEC>*)(rawt + off);
-    const TX* x0 = x0v.v;
-    const TX* xt = xtv.v;
-    VecN<TX, VEC> o0v, otv;
-    TX* o0 = o0v.v;
-    TX* ot = otv.v;
+  // rows in groups of RG: the group's loads are issued together before any of its rows is
+  // computed, so each thread keeps 2*RG row loads in flight
+  constexpr int RG = 4;
+  const long long base = row_base + (long long)(kblk * block) * Cd + c0;
+  for (int r0 = 0; r0 < block; r0 += RG) {
+    VecN<TX, VEC> x0v[RG], xtv[RG];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float c0v = round_through<TW>(to_f32(x0[e]));
-      const float ctv = round_through<TW>(to_f32(xt[e]));
-      float a0 = bv[e], at = bv[e];
-#pragma unroll
-      for (int j = 0; j < K - 1; ++j) {
-        a0 = __builtin_fmaf(wv[e][j], h0[j][e], a0);
-        at = __builtin_fmaf(wv[e][j], ht[j][e], at);
-      }
-      a0 = __builtin_fmaf(wv[e][K - 1], c0v, a0);
-      at = __builtin_fmaf(wv[e][K - 1], ctv, at);
-      a0 = round_through<TW>(a0);
-      at = round_through<TW>(at);
-      o0[e] = from_f32<TX>(round_through<TW>(silu_f32(a0)));
-      ot[e] = from_f32<TX>(round_through<TW>(silu_f32(at)));
-#pragma unroll
-      for (int j = 0; j < K - 2; ++j) { h0[j][e] = h0[j + 1][e]; ht[j][e] = ht[j + 1][e]; }
-      h0[K - 2][e] = c0v;
-      ht[K - 2][e] = ctv;
+    for (int q = 0; q < RG; ++q) {
+      const int r = min(r0 + q, block - 1);  // a ragged last group reloads the last row, unused
+      x0v[q] = *(const VecN<TX, VEC>*)(raw0 + base + (long long)r * Cd);
+      xtv[q] = *(const VecN<TX, VEC>*)(rawt + base + (long long)r * Cd);
     }
-    *(VecN<TX, VEC>*)(y0 + off) = o0v;
-    *(VecN<TX, VEC>*)(yt + off) = otv;
+#pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      if (r0 + q >= block) break;
+      const TX* x0 = x0v[q].v;
+      const TX* xt = xtv[q].v;
+      VecN<TX, VEC> o0v, otv;
+      TX* o0 = o0v.v;
+      TX* ot = otv.v;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float c0v = round_through<TW>(to_f32(x0[e]));
+        const float ctv = round_through<TW>(to_f32(xt[e]));
+        float a0 = bv[e], at = bv[e];
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) {
+          a0 = __builtin_fmaf(wv[e][j], h0[j][e], a0);
+          at = __builtin_fmaf(wv[e][j], ht[j][e], at);
+        }
+        a0 = __builtin_fmaf(wv[e][K - 1], c0v, a0);
+        at = __builtin_fmaf(wv[e][K - 1], ctv, at);
+        a0 = round_through<TW>(a0);
+        at = round_through<TW>(at);
+        o0[e] = from_f32<TX>(round_through<TW>(silu_f32(a0)));
+        ot[e] = from_f32<TX>(round_through<TW>(silu_f32(at)));
+#pragma unroll
+        for (int j = 0; j < K - 2; ++j) { h0[j][e] = h0[j + 1][e]; ht[j][e] = ht[j + 1][e]; }
+        h0[K - 2][e] = c0v;
+        ht[K - 2][e] = ctv;
+      }
+      const long long off = base + (long long)(r0 + q) * Cd;
+      *(VecN<TX, VEC>*)(y0 + off) = o0v;
+      *(VecN<TX, VEC>*)(yt + off) = otv;
+    }
   }
 }
 

@@ -2,9 +2,10 @@
 
 Drop-in for the reference's `src/dllm_qwen38/blockdiff.py`:
   block_diffusion_forward (blockdiff.py:96-203), BreakMode (:69-88), complementary_mask /
-  block_causal_mask (:43-66), and LayerStep, the per-layer unit of the FSDP trainer
-  (fsdp_train.py:83-130), which here calls the same `layer_step` function as the stack driver so
-  the fork exists in one place.
+  block_causal_mask (:43-66), the per-block oracles reference_block_logits /
+  reference_clean_logits (:206-243) and tiny_text_model (:246-278), and LayerStep, the per-layer
+  unit of the FSDP trainer (fsdp_train.py:83-130), which here calls the same `layer_step` function
+  as the stack driver so the fork exists in one place.
 
 Visibility contract (x_t = noised stream, x_0 = clean stream, block(i) = i // block):
 x_t token i sees x_t token j iff block(j) == block(i); x_t sees x_0 iff block(j) < block(i);
@@ -230,3 +231,63 @@ class LayerStep(nn.Module):
         cos2 = cos.reshape(-1, S, cos.shape[-1])[0].to(h0.dtype)
         sin2 = sin.reshape(-1, S, sin.shape[-1])[0].to(h0.dtype)
         return layer_step(self.layer, self.kind, h0, ht, block=block, cos2=cos2, sin2=sin2, fault=self.fault)
+
+
+@torch.no_grad()
+def reference_block_logits(text_model, lm_head, x0_ids: torch.Tensor, xt_ids: torch.Tensor, block: int, *,
+                           layers: int | None = None) -> torch.Tensor:
+    """Oracle (blockdiff.py:206-228): per block k, the UNMODIFIED transformers model on
+    cat([x_0 blocks < k, x_t block k]) under the block-causal 4D mask; the last block's logits,
+    concatenated over k -> [B, L, V]. Runs transformers' own modules (its torch GDN kernel and eager
+    attention) wherever the model lives; none of this module's kernels are involved."""
+    cfg = text_model.config
+    L = x0_ids.shape[1]
+    saved = cfg.num_hidden_layers
+    if layers is not None:
+        cfg.num_hidden_layers = layers
+    try:
+        outs = []
+        for k in range(L // block):
+            seq = torch.cat([x0_ids[:, : k * block], xt_ids[:, k * block: (k + 1) * block]], 1)
+            mask = block_causal_mask(seq.shape[1], block, text_model.embed_tokens.weight.dtype, seq.device)
+            hs = text_model(input_ids=seq, attention_mask={FULL: mask, LINEAR: None}, use_cache=False).last_hidden_state
+            outs.append(lm_head(hs[:, -block:]))
+        return torch.cat(outs, 1)
+    finally:
+        cfg.num_hidden_layers = saved
+
+
+@torch.no_grad()
+def reference_clean_logits(text_model, lm_head, x0_ids: torch.Tensor, block: int, *, layers: int | None = None):
+    """Oracle for the clean stream (blockdiff.py:231-243): the unmodified model on x_0 under the
+    block-causal mask."""
+    cfg = text_model.config
+    saved = cfg.num_hidden_layers
+    if layers is not None:
+        cfg.num_hidden_layers = layers
+    try:
+        mask = block_causal_mask(x0_ids.shape[1], block, text_model.embed_tokens.weight.dtype, x0_ids.device)
+        hs = text_model(input_ids=x0_ids, attention_mask={FULL: mask, LINEAR: None}, use_cache=False).last_hidden_state
+        return lm_head(hs)
+    finally:
+        cfg.num_hidden_layers = saved
+
+
+def tiny_text_model(seed: int = 0, layers: int = 8, vocab: int = 256):
+    """A random transformers Qwen3.5 text model of the reference's unit-test size (blockdiff.py:246-278):
+    hidden 64, 6 GDN + 2 attention layers, attention heads 4/2 of dim 16, GDN heads 2 key / 4 value
+    of dim 16, conv width 4, partial RoPE 0.25 with base 1e4; CPU fp32, untied lm_head."""
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextModel
+
+    torch.manual_seed(seed)
+    cfg = Qwen3_5TextConfig(
+        vocab_size=vocab, hidden_size=64, intermediate_size=128, num_hidden_layers=layers,
+        num_attention_heads=4, num_key_value_heads=2, head_dim=16, linear_num_key_heads=2,
+        linear_num_value_heads=4, linear_key_head_dim=16, linear_value_head_dim=16, linear_conv_kernel_dim=4,
+        max_position_embeddings=4096,
+        rope_parameters={"rope_theta": 10000.0, "mrope_section": [2, 1, 1], "partial_rotary_factor": 0.25},
+        attn_implementation="eager")
+    model = Qwen3_5TextModel(cfg).eval()
+    lm_head = nn.Linear(cfg.hidden_size, vocab, bias=False)
+    return model, lm_head

@@ -1,0 +1,172 @@
+"""The visibility equivalence check of the block-diffusion forward, run on the HIP path.
+
+Counterpart of the reference's `src/dllm_qwen38/equivalence.py:1-226`: same questions, same
+report, same exit codes.
+  1. the noised stream equals the oracle (the unmodified transformers model per block under the
+     block-causal mask);
+  2. the clean stream equals the unmodified model under the block-causal mask;
+  3. perturbations: x_t block k ignores x_t block k-1 and x_0 block k, and reacts to x_0 block k-1;
+  4. every deliberate fault (concat-causal-gdn / mask-leak / no-conv-prefix) turns check 1 red.
+Exit code 0 = every check passed and every fault was detected; 1 = a check failed or a fault went
+undetected; 2 = could not measure. A run that measures nothing never exits 0.
+
+The candidate is `blockdiff.block_diffusion_forward` on the device (HIP fork, HIP attention). The
+oracle is transformers' own model in fp32 on the CPU (with --dtype bfloat16, on the bf16-rounded
+weights), so the check never runs the library's kernels on both sides.
+
+    python -m dllm_qwen38_amd.equivalence [--block 32] [--nblocks 4] [--dtype float32|bfloat16]
+"""
+
+from __future__ import annotations
+
+import argparse
+import copy
+import json
+import sys
+import time
+
+import torch
+
+from .blockdiff import BreakMode, block_diffusion_forward, reference_block_logits, reference_clean_logits, tiny_text_model
+
+FAULTS = ("concat-causal-gdn", "mask-leak", "no-conv-prefix")
+
+
+def _maxdiff(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.float().cpu() - b.float().cpu()).abs().max())
+
+
+def run(cand_model, cand_head, oracle_model, oracle_head, *, block: int, nblocks: int, layers: int | None,
+        tol: float, change_floor: float, seed: int, device: str) -> dict:
+    """All checks; the candidate runs on `device`, the oracle wherever its model lives."""
+    g = torch.Generator().manual_seed(seed)
+    L = block * nblocks
+    vocab = cand_model.embed_tokens.weight.shape[0]
+    x0 = torch.randint(0, vocab, (1, L), generator=g)
+    xt = x0.clone()
+    xt[torch.rand(1, L, generator=g) < 0.5] = vocab - 1  # mask id: any existing id will do
+    odev = oracle_model.embed_tokens.weight.device
+
+    def cand(a, b, fault=None):
+        with torch.no_grad():
+            return block_diffusion_forward(cand_model, cand_head, a.to(device), b.to(device), block,
+                                           fault=fault, layers=layers)
+
+    checks: list[dict] = []
+    t0 = time.time()
+    lt, l0 = cand(x0, xt)
+    ref_t = reference_block_logits(oracle_model, oracle_head, x0.to(odev), xt.to(odev), block, layers=layers)
+    ref_0 = reference_clean_logits(oracle_model, oracle_head, x0.to(odev), block, layers=layers)
+    d = _maxdiff(lt, ref_t)
+    checks.append({"name": "noised-stream-vs-oracle", "max_abs_diff": d, "tol": tol, "pass": d <= tol})
+    d = _maxdiff(l0, ref_0)
+    checks.append({"name": "clean-stream-vs-oracle", "max_abs_diff": d, "tol": tol, "pass": d <= tol})
+
+    if nblocks >= 2:
+        worst_xt, worst_x0k, weakest = 0.0, 0.0, float("inf")
+        for k in range(1, nblocks):
+            sl, prev = slice(k * block, (k + 1) * block), slice((k - 1) * block, k * block)
+            xt2 = xt.clone()
+            xt2[:, prev] = torch.randint(0, vocab, (1, block), generator=g)
+            worst_xt = max(worst_xt, _maxdiff(lt[:, sl], cand(x0, xt2)[0][:, sl]))
+            x02 = x0.clone()
+            x02[:, sl] = torch.randint(0, vocab, (1, block), generator=g)
+            worst_x0k = max(worst_x0k, _maxdiff(lt[:, sl], cand(x02, xt)[0][:, sl]))
+            x03 = x0.clone()
+            x03[:, prev] = torch.randint(0, vocab, (1, block), generator=g)
+            weakest = min(weakest, _maxdiff(lt[:, sl], cand(x03, xt)[0][:, sl]))
+        checks.append({"name": "xt-block-k-ignores-xt-block-k-1", "max_abs_diff": worst_xt, "tol": tol,
+                       "pass": worst_xt <= tol})
+        checks.append({"name": "xt-block-k-ignores-x0-block-k", "max_abs_diff": worst_x0k, "tol": tol,
+                       "pass": worst_x0k <= tol})
+        checks.append({"name": "xt-block-k-reacts-to-x0-block-k-1", "min_abs_diff": weakest, "floor": change_floor,
+                       "pass": weakest >= change_floor})
+
+    faults = []
+    for name in FAULTS:
+        d = _maxdiff(cand(x0, xt, BreakMode(name))[0], ref_t)
+        faults.append({"fault": name, "max_abs_diff": d, "tol": tol, "detected": d > tol})
+
+    return {
+        "block": block, "nblocks": nblocks, "seq_len": L,
+        "layers": layers if layers is not None else int(cand_model.config.num_hidden_layers),
+        "layer_types": list(cand_model.config.layer_types[: layers or None]),
+        "dtype": str(cand_model.embed_tokens.weight.dtype), "device": device, "oracle_device": str(odev),
+        "seconds": round(time.time() - t0, 2), "checks": checks, "faults": faults,
+        "checks_passed": sum(c["pass"] for c in checks), "checks_total": len(checks),
+        "faults_detected": sum(f["detected"] for f in faults), "faults_total": len(faults),
+    }
+
+
+def _load(model_id: str | None, seed: int):
+    if model_id is None:
+        return tiny_text_model(seed=seed)
+    from transformers import AutoConfig, AutoModelForCausalLM, AutoModelForImageTextToText
+
+    cfg = AutoConfig.from_pretrained(model_id)
+    if getattr(cfg, "text_config", None) is not None:
+        m = AutoModelForImageTextToText.from_pretrained(model_id, dtype=torch.float32, attn_implementation="eager")
+        return m.model.language_model.eval(), m.lm_head
+    m = AutoModelForCausalLM.from_pretrained(model_id, dtype=torch.float32, attn_implementation="eager")
+    return m.model.eval(), m.lm_head
+
+
+def main(argv: list[str] | None = None) -> int:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--model", default=None, help="local checkpoint directory; omit for the tiny random model")
+    p.add_argument("--layers", type=int, default=None, help="use only the first N layers")
+    p.add_argument("--block", type=int, default=32)
+    p.add_argument("--nblocks", type=int, default=4)
+    p.add_argument("--tol", type=float, default=None, help="max |dlogit| accepted (default: fp32 1e-3, bf16 0.25)")
+    p.add_argument("--change-floor", type=float, default=None, help="min |dlogit| of a real dependency (default 10*tol)")
+    p.add_argument("--dtype", default="float32", choices=["float32", "bfloat16"])
+    p.add_argument("--device", default="cuda")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--json", default=None, help="write the report here as JSON")
+    a = p.parse_args(argv)
+
+    dtype = torch.float32 if a.dtype == "float32" else torch.bfloat16
+    tol = a.tol if a.tol is not None else (1e-3 if dtype == torch.float32 else 0.25)
+    floor = a.change_floor if a.change_floor is not None else 10 * tol
+    if a.nblocks < 1:
+        print("COULD-NOT-MEASURE nblocks < 1", file=sys.stderr)
+        return 2
+    try:
+        oracle_model, oracle_head = _load(a.model, a.seed)
+    except Exception as e:  # noqa: BLE001 - could not measure is its own exit code
+        print(f"COULD-NOT-MEASURE model load failed: {type(e).__name__}: {e}", file=sys.stderr)
+        return 2
+    if a.layers is not None and a.layers > oracle_model.config.num_hidden_layers:
+        print("COULD-NOT-MEASURE --layers exceeds the model", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available() or not str(a.device).startswith("cuda"):
+        print("COULD-NOT-MEASURE the candidate runs on the HIP kernels and needs a ROCm device", file=sys.stderr)
+        return 2
+    oracle_model.requires_grad_(False)
+    oracle_head.requires_grad_(False)
+    cand_model = copy.deepcopy(oracle_model).to(a.device, dtype)
+    cand_head = copy.deepcopy(oracle_head).to(a.device, dtype)
+    if dtype != torch.float32:  # the oracle sees the same (rounded) weights, in fp32
+        oracle_model.to(dtype).float()
+        oracle_head.to(dtype).float()
+
+    rep = run(cand_model, cand_head, oracle_model, oracle_head, block=a.block, nblocks=a.nblocks, layers=a.layers,
+              tol=tol, change_floor=floor, seed=a.seed, device=a.device)
+    rep["model"] = a.model or "tiny-random"
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(rep, f, indent=1)
+    for c in rep["checks"]:
+        val = c.get("max_abs_diff", c.get("min_abs_diff"))
+        print(f"{'PASS' if c['pass'] else 'FAIL'}\t{c['name']}\t{val:.3e}")
+    for f in rep["faults"]:
+        print(f"{'DETECTED' if f['detected'] else 'UNDETECTED'}\tfault:{f['fault']}\t{f['max_abs_diff']:.3e}")
+    print(f"CHECKS\t{rep['checks_passed']}/{rep['checks_total']}\tFAULTS-DETECTED\t{rep['faults_detected']}/"
+          f"{rep['faults_total']}\tmodel={rep['model']} layers={rep['layers']} L={rep['seq_len']} dtype={rep['dtype']} "
+          f"{rep['seconds']}s")
+    ok = rep["checks_passed"] == rep["checks_total"] and rep["faults_detected"] == rep["faults_total"]
+    return 0 if ok else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -173,3 +173,19 @@ def test_27b_class_visibility_invariances_bit_exact(stack27, dev):
     assert torch.equal(l0_c[:, : k * block], l0[:, : k * block])
     assert torch.equal(lt_c[:, : (k + 1) * block], lt[:, : (k + 1) * block])
     assert not torch.equal(lt_c[:, (k + 1) * block:], lt[:, (k + 1) * block:])
+
+
+def test_equivalence_harness_passes_and_detects_every_fault(dev, tmp_path):
+    """The reference's harness contract on the HIP path: 5/5 checks, 3/3 faults, exit 0."""
+    import json
+
+    from dllm_qwen38_amd import equivalence
+
+    out = tmp_path / "eq.json"
+    assert equivalence.main(["--block", "8", "--nblocks", "4", "--json", str(out)]) == 0
+    rep = json.loads(out.read_text())
+    assert rep["checks_passed"] == rep["checks_total"] == 5
+    assert rep["faults_detected"] == rep["faults_total"] == 3
+    out16 = tmp_path / "eq16.json"
+    assert equivalence.main(["--dtype", "bfloat16", "--block", "16", "--nblocks", "4", "--change-floor", "1e-3",
+                             "--json", str(out16)]) == 0

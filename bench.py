@@ -81,11 +81,19 @@ def main(argv=None):
     ap.add_argument("--calibration-copy-gib", type=float, default=0.0,
                     help="after the timed steps, copy this many GiB device-to-device (the reference transfer "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--workload", default="gdn-layer", choices=["gdn-layer", "attention", "stack"],
+                    help="gdn-layer (default, the headline metric); attention: the complementary-mask attention "
+                         "layer kernel at B=2 L=4096 Hq=24 Hkv=4 d=256; stack: the 16-layer 27B-class "
+                         "two-stream forward at B=1 L=2048")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the state-fork layer shards over (batch, value head) with no "
               "exchange, and this build runs and reports the single-GPU share; use --gpus 1", file=sys.stderr)
         return 2
+    if a.workload == "attention":
+        return bench_attention(a)
+    if a.workload == "stack":
+        return bench_stack(a)
 
     import torch
 
@@ -163,6 +171,144 @@ def main(argv=None):
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(a.cpu_sample_L, a.cpu_budget_s)
         res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
+    print(json.dumps(res))
+    return 0
+
+
+def _timed(fn, steps, warmup, stream):
+    """Run fn warmup times, then time exactly `steps` runs between HIP events on `stream`."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
+
+
+def bench_attention(a):
+    """Complementary-mask attention over cat([x_t, x_0]) at B=2 L=4096 block 32, Hq=24 Hkv=4 d=256
+    (bf16 Q/K/V ~ N(0,1)/16, rotary already applied). Roofline: MFMA, on the visible pairs only."""
+    import torch
+
+    from dllm_qwen38_amd import attention
+
+    B, L, Hq, Hkv, d, block = 2, 4096, 24, 4, 256, 32
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(407)
+    q = (torch.randn(B, 2 * L, Hq, d, generator=g) / 16).to(torch.bfloat16).to(dev)
+    k = (torch.randn(B, 2 * L, Hkv, d, generator=g) / 16).to(torch.bfloat16).to(dev)
+    v = (torch.randn(B, 2 * L, Hkv, d, generator=g) / 16).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream(dev)
+    ms, wall = _timed(lambda: attention.bd_attention(q, k, v, block=block, out=out), a.steps, a.warmup, stream)
+    fl = attention.attention_flops(B, L, Hq, d, block)
+    tf = fl / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "complementary-mask attention layer tokens/s (B*L clean positions); % bf16 MFMA roofline",
+        "value": B * L / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/16 q, k, v)",
+        "config": {"workload": "complementary-mask attention, B=2 L=4096 block 32 Hq=24 Hkv=4 d=256 over "
+                               "cat([x_t, x_0]), bf16", "global_batch": B, "seq_len": L, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tf / BF16_MFMA_PEAK_TFLOPS, "traffic": None},
+        "algorithmic_gflop": fl / 1e9, "wall_s_timed": wall, "cpu_baseline": None,
+    }
+    if not a.no_cpu_baseline:
+        sys.path.insert(0, ROOT)
+        from oracle import attn_ref
+
+        n = len(os.sched_getaffinity(0))
+        torch.set_num_threads(n)
+        Ls = 512
+        qs, ks, vs = (t[:1].cpu() for t in (q, k, v))
+        qs = torch.cat([qs[:, :Ls], qs[:, L:L + Ls]], 1)
+        ks = torch.cat([ks[:, :Ls], ks[:, L:L + Ls]], 1)
+        vs = torch.cat([vs[:, :Ls], vs[:, L:L + Ls]], 1)
+        attn_ref.bd_attention(qs, ks, vs, block=block)
+        times = []
+        start = time.perf_counter()
+        while len(times) < 3 or time.perf_counter() - start < a.cpu_budget_s:
+            t = time.perf_counter()
+            attn_ref.bd_attention(qs, ks, vs, block=block)
+            times.append(time.perf_counter() - t)
+        med = statistics.median(times)
+        res["cpu_baseline"] = {"value": Ls / med, "unit": "tokens/s", "cores": n, "kind": "port",
+                               "sample": f"B=1 L={Ls} (the first {Ls} positions of each half), same heads and d, "
+                                         f"fp32 torch CPU oracle; median of {len(times)} runs ({med:.2f} s/run)"}
+    print(json.dumps(res))
+    return 0
+
+
+def _stack_flops(model, lm_head, B, L, block):
+    """Algorithmic flops of one two-stream forward: every linear layer on 2*B*L token rows, the GDN
+    chunk contractions and the attention over visible pairs."""
+    from torch import nn
+
+    from dllm_qwen38_amd import attention, gdn
+
+    rows = 2 * B * L
+    lin = sum(m.in_features * m.out_features for m in model.modules() if isinstance(m, nn.Linear))
+    lin += lm_head.in_features * lm_head.out_features
+    c = model.config
+    n_gdn = sum(t == "linear_attention" for t in c.layer_types)
+    n_att = len(c.layer_types) - n_gdn
+    return (2 * rows * lin + n_gdn * gdn.layer_flops(B, L, c.linear_num_value_heads, c.linear_key_head_dim,
+                                                      c.linear_value_head_dim, block)
+            + n_att * attention.attention_flops(B, L, c.num_attention_heads, c.head_dim, block))
+
+
+def bench_stack(a):
+    """The two-stream block-diffusion forward of a 16-layer 27B-class stack (12 GDN + 4 attention,
+    hidden 5120, vocab 151936) at B=1 L=2048 block 32, bf16, seeded N(0, 0.02) weights on the device,
+    logits of both streams. Roofline: MFMA over the whole forward's algorithmic flops."""
+    import torch
+
+    from dllm_qwen38_amd import blockdiff
+    from dllm_qwen38_amd import model as hybrid
+
+    B, L, block = 1, 2048, 32
+    dev = torch.device("cuda:0")
+    c = hybrid.config_27b_truncated(layers=16)
+    model, lm_head = hybrid.build(c, device=dev, dtype=torch.bfloat16, seed=513)
+    model.requires_grad_(False)
+    lm_head.requires_grad_(False)
+    g = torch.Generator().manual_seed(510)
+    x0 = torch.randint(0, c.vocab_size, (B, L), generator=g)
+    xt = x0.clone()
+    tb = torch.rand(B, L // block, generator=g).repeat_interleave(block, 1)
+    xt[torch.rand(B, L, generator=g) < tb] = c.vocab_size - 1
+    x0, xt = x0.to(dev), xt.to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        with torch.inference_mode():
+            blockdiff.block_diffusion_forward(model, lm_head, x0, xt, block)
+
+    steps = max(1, min(a.steps, 10))
+    ms, wall = _timed(step, steps, max(1, min(a.warmup, 2)), stream)
+    fl = _stack_flops(model, lm_head, B, L, block)
+    tf = fl / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "two-stream block-diffusion forward tokens/s (B*L clean positions), 16-layer 27B-class stack",
+        "value": B * L / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": max(1, min(a.warmup, 2)),
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, uniform ids, per-block masking with mask id V-1)",
+        "config": {"workload": "block_diffusion_forward, 16 layers (12 GDN + 4 attention) hidden 5120 MLP 17408 "
+                               "vocab 151936, B=1 L=2048 block 32, logits of both streams", "global_batch": B,
+                   "seq_len": L, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tf / BF16_MFMA_PEAK_TFLOPS, "traffic": None},
+        "algorithmic_tflop": fl / 1e12, "params": hybrid.param_count(model) + lm_head.weight.numel(),
+        "wall_s_timed": wall, "cpu_baseline": None,
+    }
     print(json.dumps(res))
     return 0
 

@@ -357,6 +357,267 @@ static int launch_attn(const AttnArgs& a, hipStream_t st) {
   return DLLM_OK;
 }
 
+// ---------------------------------------------------------------------------------------------
+// bf16, d == D in {64, 128, 256}: eight waves, two per 32-query tile. Both waves of a pair form
+// the whole S^T = K Q^T (lane = query) and take the same softmax decisions; wave e = 0 / 1 of the
+// pair accumulates d half e of O^T, so a wave holds all of Q but only half of O and the kernel
+// runs two waves per SIMD. (Splitting S between the pair instead needs an LDS exchange and a second
+// barrier per tile, which measured slower than computing S twice.)
+// K and V tiles travel global -> LDS by direct loads, no registers: each wave instruction moves
+// 1 KB = 64 lanes x 16 bytes; rows are dense with their 16-byte chunks XOR-swizzled by row so that
+// the K fragment reads and the V^T transpose reads are free of bank conflicts. A ring of NST
+// stages keeps NST - 1 tiles in flight ahead of the one being computed; one barrier per tile.
+// ---------------------------------------------------------------------------------------------
+template <int D>
+struct DmaSmem {
+  static constexpr int NST = 4;                  // ring stages
+  static constexpr int TILE_BYTES = 32 * D * 2;  // one K or V tile
+  static constexpr int STAGE = 2 * TILE_BYTES;   // K, then V
+  static constexpr int TOTAL = NST * STAGE;
+};
+
+template <int D>
+__device__ __forceinline__ int swz_off(int row, int col) {  // byte offset of (row, col) in a swizzled tile
+  constexpr int CH = D / 8;
+  return row * (2 * D) + (((col >> 3) ^ (row & (CH - 1))) << 4) + ((col & 7) << 1);
+}
+
+// s_waitcnt with vmcnt(N) and the other counters unconstrained (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+template <int D>
+__global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
+  using SM = DmaSmem<D>;
+  using F = Frag<true>;
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  constexpr int NST = SM::NST;
+  constexpr int CH = D / 8;          // 16-byte chunks per row
+  constexpr int DT = D / 32;         // 32-wide slices of d
+  constexpr int DH = D / 2;          // this wave's half of d for O
+  constexpr int SH = DH / 32;
+  constexpr int RPI = 64 / CH;       // rows per 1 KB wave instruction
+  constexpr int IPT = 32 / RPI;      // wave instructions per K (or V) tile
+  constexpr int IPW = 2 * IPT / 8;   // per wave per tile
+  static_assert(IPW >= 1 && (2 * IPT) % 8 == 0, "tile must split evenly over eight waves");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int pair = wave >> 1, e = wave & 1;
+  const int L = a.L, C = a.C;
+  const int ntq = (L + 31) >> 5;
+  const int ng = (ntq + 3) >> 2;
+  const int rep = a.Hq / a.Hkv;
+
+  const int lin = xcd_linear_id_attn(blockIdx.x, gridDim.x);
+  const int per_g = 2 * a.B * a.Hkv * rep;
+  const int g = ng - 1 - lin / per_g;
+  int rem = lin % per_g;
+  const int qh = rem % 2;
+  rem /= 2;
+  const int hr = rem % rep;
+  rem /= rep;
+  const int hkv = rem % a.Hkv;
+  const int b = rem / a.Hkv;
+  const int hq = hkv * rep + hr;
+
+  const int g0 = g * 128, g1 = min(L, g0 + 128);
+  const int r0 = g0 + pair * 32, r1 = min(L, r0 + 32);
+  const bool wave_live = r0 < L;
+  const int qb0 = r0 / C, qb1 = (max(r0, r1 - 1)) / C;
+  const int gqb0 = g0 / C, gqb1 = (g1 - 1) / C;
+  int lo0, hi0, lo1, hi1;
+  if (qh == 1) {
+    lo0 = hi0 = 0;
+    lo1 = 0;
+    hi1 = min(L, (gqb1 + 1) * C);
+  } else {
+    lo0 = a.leak ? 0 : gqb0 * C;
+    hi0 = min(L, (gqb1 + 1) * C);
+    lo1 = 0;
+    hi1 = min(L, gqb1 * C);
+  }
+  const int t0lo = lo0 >> 5, t0hi = (hi0 + 31) >> 5;
+  const int t1lo = lo1 >> 5, t1hi = (hi1 + 31) >> 5;
+  const int n0 = hi0 > lo0 ? t0hi - t0lo : 0;
+  const int n1 = hi1 > lo1 ? t1hi - t1lo : 0;
+  const int ntiles = n0 + n1;
+  auto tile_pos = [&](int n, int& kh, int& j0) {
+    if (n < n1) { kh = 1; j0 = (t1lo + n) * 32; }
+    else { kh = 0; j0 = (t0lo + n - n1) * 32; }
+  };
+
+  const bf16* const qbase = (const bf16*)a.q + b * a.q_sb + (long long)hq * a.q_sh;
+  const bf16* const kbase = (const bf16*)a.k + b * a.k_sb + (long long)hkv * a.k_sh;
+  const bf16* const vbase = (const bf16*)a.v + b * a.v_sb + (long long)hkv * a.v_sh;
+
+  // Q^T fragments (lane = query), kept in registers. S contracts over d, and neither operand of
+  // K Q^T is an accumulator, so both use contiguous d runs: the first MFMA of slice s takes
+  // d = 32s + 8h .. +7, the second 32s + 16 + 8h .. +7 (16-byte loads, 16-byte LDS reads).
+  F qf[DT];
+  {
+    const int row = min(r0 + l32, L - 1);
+    const bf16* qp = qbase + (long long)(qh * L + row) * a.q_st;
+#pragma unroll
+    for (int s = 0; s < DT; ++s) {
+      qf[s].lo = *(const bf16x8*)(qp + 32 * s + 8 * h);
+      qf[s].hi = *(const bf16x8*)(qp + 32 * s + 16 + 8 * h);
+    }
+  }
+  wait_vmcnt<0>();  // only the direct loads below are counted inside the loop
+
+  // direct global -> LDS staging of K and V tile n into its ring stage (this wave's IPW loads)
+  auto stage_tile = [&](int n) {
+    int kh, j0;
+    tile_pos(n, kh, j0);
+    unsigned char* const sb = smem + (n % NST) * SM::STAGE;
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+      const int gi = wave * IPW + j;  // wave-uniform
+      const bool isv = gi >= IPT;
+      const int row0 = (gi % IPT) * RPI;
+      const int row = row0 + lane / CH;
+      const int chunk = (lane % CH) ^ (row & (CH - 1));
+      const int key = min(j0 + row, L - 1);  // rows past L load a valid row; they are masked
+      const long long off = (long long)(kh * L + key) * (isv ? a.v_st : a.k_st) + chunk * 8;
+      const bf16* src = (isv ? vbase : kbase) + off;
+      unsigned char* dst = sb + (isv ? SM::TILE_BYTES : 0) + row0 * (2 * D);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+    }
+  };
+  // wait until tile n's loads (this wave's) have landed, given which later tiles were issued
+  auto wait_tile = [&](int n) {
+    const int ahead = min(NST - 2, ntiles - 1 - n);  // tiles issued after n and still allowed in flight
+    if (ahead >= 2) wait_vmcnt<2 * IPW>();
+    else if (ahead == 1) wait_vmcnt<IPW>();
+    else wait_vmcnt<0>();
+  };
+
+  f32x16 O[SH];
+#pragma unroll
+  for (int t = 0; t < SH; ++t) O[t] = zero16();
+  float mrow = -1e30f, lrow = 0.f;
+  static_assert(NST == 4, "wait_tile assumes up to two tiles in flight behind the waited one");
+
+#pragma unroll
+  for (int n = 0; n < NST - 1; ++n)
+    if (n < ntiles) stage_tile(n);
+  if (ntiles > 0) wait_tile(0);
+  __syncthreads();
+  for (int n = 0; n < ntiles; ++n) {
+    if (n + NST - 1 < ntiles) stage_tile(n + NST - 1);  // its stage held tile n - 1, done before the barrier
+    int kh, j0;
+    tile_pos(n, kh, j0);
+    const int kb0 = j0 / C, kb1 = (min(L, j0 + 32) - 1) / C;
+    bool any = false, all = false;
+    if (wave_live) classify(qh, qb0, qb1, kh, kb0, kb1, a.leak, any, all);
+    const bool ragged = (j0 + 32 > L) || (r1 - r0 < 32);
+    const unsigned char* Ks = smem + (n % NST) * SM::STAGE;
+    const unsigned char* Vs = Ks + SM::TILE_BYTES;
+    if (any) {
+      // S^T = K Q^T: rows = keys (lane l32 reads key row l32), k = d
+      f32x16 st = zero16();
+#pragma unroll
+      for (int s = 0; s < DT; ++s) {
+        F kf;
+        kf.lo = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 8 * h));
+        kf.hi = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 16 + 8 * h));
+        mma32(st, kf, qf[s]);
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;
+      if (!all || ragged) {
+        const int qi = r0 + l32;
+        const int qbl = qi / C;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int kj = j0 + rho(v, h);
+          const bool okk = kj < L && qi < L && visible(qh, qbl, kh, kj / C, a.leak);
+          st[v] = okk ? st[v] : -INFINITY;
+        }
+      }
+      float mx = st[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, st[v]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // lazy rescale (see bd_attn_kernel)
+      constexpr float RESCALE_LOG2 = 8.f;
+      if (__builtin_amdgcn_ballot_w64(mx > mrow + RESCALE_LOG2) != 0) {
+        const float mnew = fmaxf(mrow, mx);
+        const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+#pragma unroll
+        for (int t = 0; t < SH; ++t)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) O[t][v] *= alpha;
+        lrow *= alpha;
+        mrow = mnew;
+      }
+      float ps = 0.f;
+      f32x16 p;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        p[v] = __builtin_amdgcn_exp2f(st[v] - mrow);
+        ps += p[v];
+      }
+      ps += __shfl_xor(ps, 32);
+      lrow += ps;
+      F pf;
+      acc_to_frag(p, pf);
+      // O^T (this wave's d half) += V^T P^T; V^T fragments by transpose reads of the swizzled rows
+      const int sl = lane & 15;
+      const int krow = 4 * h + (sl >> 2);                      // + 8m
+      const int dcol = 16 * ((lane >> 4) & 1) + 4 * (sl & 3);  // + d0
+#pragma unroll
+      for (int t = 0; t < SH; ++t) {
+        const int d0 = e * DH + 32 * t;
+        bf16x4 r[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          r[m] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(Vs + swz_off<D>(8 * m + krow, d0 + dcol)));
+        F vf;
+        vf.lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+        vf.hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
+        mma32(O[t], vf, pf);
+      }
+    }
+    if (n + 1 < ntiles) wait_tile(n + 1);
+    __syncthreads();  // tile n + 1 staged by every wave; every wave is done with tile n's stage
+  }
+
+  const int qi = r0 + l32;
+  if (wave_live && qi < L) {
+    const float inv = 1.f / lrow;
+    bf16* op = (bf16*)a.out + (((long long)b * 2 * L + qh * L + qi) * a.Hq + hq) * a.d + e * DH;
+#pragma unroll
+    for (int t = 0; t < SH; ++t)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        bf16x4 o4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o4[i] = (bf16)(O[t][4 * m + i] * inv);
+        *(bf16x4*)(op + 32 * t + 8 * m + 4 * h) = o4;
+      }
+  }
+}
+
+template <int D>
+static int launch_attn_dma(const AttnArgs& a, hipStream_t st) {
+  const int ntq = (a.L + 31) / 32;
+  const int ng = (ntq + 3) / 4;
+  const long long nblk = (long long)ng * 2 * a.B * a.Hq;
+  if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "attention: grid too large");
+  bd_attn_dma_kernel<D><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention launch: %s", hipGetErrorString(e));
+  return DLLM_OK;
+}
+
 static bool fits32(long long x) { return x >= -2147483647LL && x <= 2147483647LL; }
 
 }  // namespace dllm
@@ -396,6 +657,14 @@ extern "C" int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, co
   a.vec = vec;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DT_BF16) {
+    // the direct-load kernel needs whole 16-byte rows of exactly d elements (vectorisable layout)
+    if (vec && d == dw && dw >= 64 && (a.k_st % 8) == 0 && (a.v_st % 8) == 0) {
+      switch (dw) {
+        case 64: return launch_attn_dma<64>(a, st);
+        case 128: return launch_attn_dma<128>(a, st);
+        default: return launch_attn_dma<256>(a, st);
+      }
+    }
     switch (dw) {
       case 32: return launch_attn<32, true>(a, st);
       case 64: return launch_attn<64, true>(a, st);

@@ -1,0 +1,299 @@
+// Row-wise prologue / epilogue kernels around the two mixers (gfx950): the Qwen3.5 RMSNorm with a
+// (1 + w) weight (optionally fused with the residual add before it), the gated RMSNorm of the GDN
+// output, the SwiGLU product of the MLP, and the attention prologue (per-head q/k RMSNorm followed
+// by partial RoPE with positions shared by both halves of cat([x_t, x_0])).
+//
+// These are HBM-bound: one wave per row, every input read once, fp32 arithmetic, and results
+// rounded at the cast points of the transformers modules they replace so that bf16 results match
+// them element for element except where a fp32 reduction order differs.
+#include "common.h"
+
+namespace dllm {
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <typename T> __device__ __forceinline__ float ld(const T* p) { return to_f32(*p); }
+
+// y = rmsnorm(s) * (1 + w) with s = x (+ r, rounded to T, also written to sum_out)
+template <typename T, typename TW, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x, const T* __restrict__ r,
+                                                      T* __restrict__ sum_out, const TW* __restrict__ w,
+                                                      T* __restrict__ y, int rows, int dim, float eps, int unit) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const long long base = (long long)row * dim;
+  // NV > 0: dim == 64 * 8 * NV, 16-byte vectors; NV == 0: generic strided scalar path
+  if constexpr (NV > 0) {
+    typedef __attribute__((ext_vector_type(8))) T V8;
+    float v[NV][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const long long off = base + (long long)(k * 64 + lane) * 8;
+      const V8 xv = *(const V8*)(x + off);
+      V8 sv = xv;
+      if (r) {
+        const V8 rv = *(const V8*)(r + off);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sv[i] = from_f32<T>(to_f32(xv[i]) + to_f32(rv[i]));
+        if (sum_out) *(V8*)(sum_out + off) = sv;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[k][i] = to_f32(sv[i]);
+        ss = __builtin_fmaf(v[k][i], v[k][i], ss);
+      }
+    }
+    const float inv = rsqrtf(wave_sum(ss) / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c0 = (k * 64 + lane) * 8;
+      V8 yv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float wf = to_f32(w[c0 + i]);
+        yv[i] = from_f32<T>(v[k][i] * inv * (unit ? 1.f + wf : wf));
+      }
+      *(V8*)(y + base + c0) = yv;
+    }
+  } else {
+    float ss = 0.f;
+    for (int c = lane; c < dim; c += 64) {
+      float s = ld(x + base + c);
+      if (r) {
+        const T st = from_f32<T>(s + ld(r + base + c));
+        if (sum_out) sum_out[base + c] = st;
+        s = to_f32(st);
+      }
+      ss = __builtin_fmaf(s, s, ss);
+    }
+    const float inv = rsqrtf(wave_sum(ss) / (float)dim + eps);
+    for (int c = lane; c < dim; c += 64) {
+      const float s = r ? to_f32(from_f32<T>(ld(x + base + c) + ld(r + base + c))) : ld(x + base + c);
+      const float wf = to_f32(w[c]);
+      y[base + c] = from_f32<T>(s * inv * (unit ? 1.f + wf : wf));
+    }
+  }
+}
+
+// y = (w * round_T(rmsnorm(x))) * silu(z), the product rounded to T at each step as in the module
+template <typename T, typename TW>
+__global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict__ x, const T* __restrict__ z,
+                                                            const TW* __restrict__ w, T* __restrict__ y, int rows,
+                                                            int dim, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const long long base = (long long)row * dim;
+  float ss = 0.f;
+  for (int c = lane; c < dim; c += 64) {
+    const float v = ld(x + base + c);
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  const float inv = rsqrtf(wave_sum(ss) / (float)dim + eps);
+  for (int c = lane; c < dim; c += 64) {
+    const float t = round_through<T>(ld(x + base + c) * inv);
+    const float u = round_through<T>(to_f32(w[c]) * t);  // weight (module dtype) * normed (input dtype)
+    y[base + c] = from_f32<T>(u * silu_f32(ld(z + base + c)));
+  }
+}
+
+// out = round_T(round_T(silu(g)) * u)
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ g, const T* __restrict__ u,
+                                                     T* __restrict__ out, long long n) {
+  typedef __attribute__((ext_vector_type(8))) T V8;
+  const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    const V8 gv = *(const V8*)(g + i), uv = *(const V8*)(u + i);
+    V8 o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = from_f32<T>(round_through<T>(silu_f32(to_f32(gv[k]))) * to_f32(uv[k]));
+    *(V8*)(out + i) = o;
+  } else {
+    for (long long k = i; k < n; ++k) out[k] = from_f32<T>(round_through<T>(silu_f32(to_f32(g[k]))) * to_f32(u[k]));
+  }
+}
+
+// Attention prologue: one wave per (token, head) row of q (then k). rmsnorm over the head dim with
+// (1 + w), then RoPE on the first rd dims: out = a*cos + rotate_half(a)*sin with every product and
+// the sum rounded to T (the module computes them in the activation dtype). Token t of the
+// 2L-long sequence uses table row t mod L.
+template <typename T, typename TW>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const T* __restrict__ q, long long q_sb, int q_st, int q_sh, const T* __restrict__ k, long long k_sb, int k_st,
+    int k_sh, const TW* __restrict__ wq, const TW* __restrict__ wk, const T* __restrict__ cosb,
+    const T* __restrict__ sinb, T* __restrict__ qo, T* __restrict__ ko, int B, int S, int L, int Hq, int Hkv, int hd,
+    int rd, float eps) {
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const long long nq = (long long)B * S * Hq, nk = (long long)B * S * Hkv;
+  if (row >= nq + nk) return;
+  const bool isq = row < nq;
+  const long long rr = isq ? row : row - nq;
+  const int H = isq ? Hq : Hkv;
+  const int hh = (int)(rr % H);
+  const long long bt = rr / H;
+  const int t = (int)(bt % S), b = (int)(bt / S);
+  const T* src = isq ? q + b * q_sb + (long long)t * q_st + (long long)hh * q_sh
+                     : k + b * k_sb + (long long)t * k_st + (long long)hh * k_sh;
+  const TW* w = isq ? wq : wk;
+  T* dst = (isq ? qo : ko) + rr * hd;
+  constexpr int MAXE = 4;  // hd <= 256
+  float v[MAXE];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int c = lane + 64 * e;
+    v[e] = c < hd ? ld(src + c) : 0.f;
+    ss = __builtin_fmaf(v[e], v[e], ss);
+  }
+  const float inv = rsqrtf(wave_sum(ss) / (float)hd + eps);
+  const int pos = t % L;
+  const int half = rd / 2;
+  // normalised values, rounded to T, then exchanged through the wave for rotate_half
+  float nv[MAXE];
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int c = lane + 64 * e;
+    nv[e] = c < hd ? round_through<T>(v[e] * inv * (1.f + to_f32(w[c]))) : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int c = lane + 64 * e;
+    // partner column for rotate_half inside the first rd dims
+    const int pc = c < half ? c + half : c - half;
+    const int pe = pc >> 6, pl = pc & 63;
+    float pv = 0.f;
+#pragma unroll
+    for (int f = 0; f < MAXE; ++f) {
+      const float x = __shfl(nv[f], pl);
+      pv = (f == pe) ? x : pv;
+    }
+    if (c < hd) {
+      float o = nv[e];
+      if (c < rd) {
+        const float cs = to_f32(cosb[(long long)pos * rd + c]), sn = to_f32(sinb[(long long)pos * rd + c]);
+        const float rot = c < half ? -pv : pv;
+        o = round_through<T>(round_through<T>(nv[e] * cs) + round_through<T>(rot * sn));
+      }
+      dst[c] = from_f32<T>(o);
+    }
+  }
+}
+
+}  // namespace dllm
+
+using namespace dllm;
+
+template <typename T, typename TW>
+static int launch_rmsnorm(const void* x, const void* r, void* so, const void* w, void* y, int rows, int dim, float eps,
+                          int unit, bool vec, hipStream_t st) {
+  const dim3 grid((rows + 3) / 4), block(256);
+  const int nv = vec && dim % 512 == 0 && dim / 512 <= 16 ? dim / 512 : 0;
+  switch (nv) {
+#define DLLM_RMS_CASE(N) \
+  case N: rmsnorm_kernel<T, TW, N><<<grid, block, 0, st>>>((const T*)x, (const T*)r, (T*)so, (const TW*)w, (T*)y, rows, dim, eps, unit); break;
+    DLLM_RMS_CASE(0) DLLM_RMS_CASE(1) DLLM_RMS_CASE(2) DLLM_RMS_CASE(3) DLLM_RMS_CASE(4) DLLM_RMS_CASE(5)
+    DLLM_RMS_CASE(6) DLLM_RMS_CASE(7) DLLM_RMS_CASE(8) DLLM_RMS_CASE(9) DLLM_RMS_CASE(10) DLLM_RMS_CASE(11)
+    DLLM_RMS_CASE(12) DLLM_RMS_CASE(13) DLLM_RMS_CASE(14) DLLM_RMS_CASE(15) DLLM_RMS_CASE(16)
+#undef DLLM_RMS_CASE
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "rmsnorm launch: %s", hipGetErrorString(e));
+}
+
+extern "C" int dllm_rmsnorm_fwd(const void* x, const void* residual, void* sum_out, const void* weight, void* y,
+                                int rows, int dim, float eps, int dtype, int dtype_w, int unit_offset, void* stream) {
+  if (!x || !weight || !y) return fail(DLLM_EINVAL, "rmsnorm: null pointer");
+  if (rows < 0 || dim <= 0) return fail(DLLM_EINVAL, "rmsnorm: bad sizes rows=%d dim=%d", rows, dim);
+  if (sum_out && !residual) return fail(DLLM_EINVAL, "rmsnorm: sum_out needs a residual");
+  if (rows == 0) return DLLM_OK;
+  const bool vec = ((uintptr_t)x | (uintptr_t)y | (uintptr_t)residual | (uintptr_t)sum_out) % 16 == 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16 && dtype_w == DT_BF16)
+    return launch_rmsnorm<bf16, bf16>(x, residual, sum_out, weight, y, rows, dim, eps, unit_offset, vec, st);
+  if (dtype == DT_BF16 && dtype_w == DT_F32)
+    return launch_rmsnorm<bf16, float>(x, residual, sum_out, weight, y, rows, dim, eps, unit_offset, vec, st);
+  if (dtype == DT_F32 && dtype_w == DT_F32)
+    return launch_rmsnorm<float, float>(x, residual, sum_out, weight, y, rows, dim, eps, unit_offset, vec, st);
+  return fail(DLLM_EUNSUPPORTED, "rmsnorm: dtype pair (%d, %d) not supported", dtype, dtype_w);
+}
+
+extern "C" int dllm_gated_rmsnorm_fwd(const void* x, const void* z, const void* weight, void* y, int rows, int dim,
+                                      float eps, int dtype, int dtype_w, void* stream) {
+  if (!x || !z || !weight || !y) return fail(DLLM_EINVAL, "gated rmsnorm: null pointer");
+  if (rows < 0 || dim <= 0) return fail(DLLM_EINVAL, "gated rmsnorm: bad sizes rows=%d dim=%d", rows, dim);
+  if (rows == 0) return DLLM_OK;
+  const dim3 grid((rows + 3) / 4), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16 && dtype_w == DT_BF16)
+    gated_rmsnorm_kernel<bf16, bf16><<<grid, block, 0, st>>>((const bf16*)x, (const bf16*)z, (const bf16*)weight,
+                                                            (bf16*)y, rows, dim, eps);
+  else if (dtype == DT_F32 && dtype_w == DT_F32)
+    gated_rmsnorm_kernel<float, float><<<grid, block, 0, st>>>((const float*)x, (const float*)z,
+                                                              (const float*)weight, (float*)y, rows, dim, eps);
+  else
+    return fail(DLLM_EUNSUPPORTED, "gated rmsnorm: dtype pair (%d, %d) not supported", dtype, dtype_w);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "gated rmsnorm launch: %s", hipGetErrorString(e));
+}
+
+extern "C" int dllm_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+  if (!gate || !up || !out) return fail(DLLM_EINVAL, "swiglu: null pointer");
+  if (n < 0) return fail(DLLM_EINVAL, "swiglu: bad size %lld", n);
+  if (n == 0) return DLLM_OK;
+  if (((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) % 16)
+    return fail(DLLM_EINVAL, "swiglu: pointers must be 16-byte aligned");
+  const long long nb = (n + 8 * 256 - 1) / (8 * 256);
+  if (nb > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "swiglu: too large");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16)
+    swiglu_kernel<bf16><<<dim3((unsigned)nb), dim3(256), 0, st>>>((const bf16*)gate, (const bf16*)up, (bf16*)out, n);
+  else if (dtype == DT_F32)
+    swiglu_kernel<float><<<dim3((unsigned)nb), dim3(256), 0, st>>>((const float*)gate, (const float*)up, (float*)out, n);
+  else
+    return fail(DLLM_EUNSUPPORTED, "swiglu: dtype %d not supported", dtype);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "swiglu launch: %s", hipGetErrorString(e));
+}
+
+extern "C" int dllm_qk_norm_rope_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                     const void* q_norm_w, const void* k_norm_w, const void* cos_table,
+                                     const void* sin_table, void* q_out, void* k_out, int B, int S, int L, int Hq,
+                                     int Hkv, int head_dim, int rotary_dim, float eps, int dtype, int dtype_w,
+                                     void* stream) {
+  if (!q || !k || !q_strides || !k_strides || !q_norm_w || !k_norm_w || !q_out || !k_out)
+    return fail(DLLM_EINVAL, "qk norm rope: null pointer");
+  if (B <= 0 || S <= 0 || L <= 0 || Hq <= 0 || Hkv <= 0 || head_dim <= 0 || head_dim > 256 || rotary_dim < 0 ||
+      rotary_dim > head_dim || (rotary_dim & 1))
+    return fail(DLLM_EINVAL, "qk norm rope: bad sizes B=%d S=%d L=%d Hq=%d Hkv=%d hd=%d rd=%d", B, S, L, Hq, Hkv,
+                head_dim, rotary_dim);
+  if (rotary_dim > 0 && (!cos_table || !sin_table)) return fail(DLLM_EINVAL, "qk norm rope: null rotary table");
+  for (int i = 1; i < 3; ++i)
+    if (q_strides[i] > 0x7fffffff || k_strides[i] > 0x7fffffff)
+      return fail(DLLM_EUNSUPPORTED, "qk norm rope: token/head strides exceed 32 bits");
+  const long long rows = (long long)B * S * (Hq + Hkv);
+  const long long nb = (rows + 3) / 4;
+  if (nb > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "qk norm rope: too large");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16 && dtype_w == DT_BF16)
+    qk_norm_rope_kernel<bf16, bf16><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+        (const bf16*)q, q_strides[0], (int)q_strides[1], (int)q_strides[2], (const bf16*)k, k_strides[0],
+        (int)k_strides[1], (int)k_strides[2], (const bf16*)q_norm_w, (const bf16*)k_norm_w, (const bf16*)cos_table,
+        (const bf16*)sin_table, (bf16*)q_out, (bf16*)k_out, B, S, L, Hq, Hkv, head_dim, rotary_dim, eps);
+  else if (dtype == DT_F32 && dtype_w == DT_F32)
+    qk_norm_rope_kernel<float, float><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+        (const float*)q, q_strides[0], (int)q_strides[1], (int)q_strides[2], (const float*)k, k_strides[0],
+        (int)k_strides[1], (int)k_strides[2], (const float*)q_norm_w, (const float*)k_norm_w, (const float*)cos_table,
+        (const float*)sin_table, (float*)q_out, (float*)k_out, B, S, L, Hq, Hkv, head_dim, rotary_dim, eps);
+  else
+    return fail(DLLM_EUNSUPPORTED, "qk norm rope: dtype pair (%d, %d) not supported", dtype, dtype_w);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "qk norm rope launch: %s", hipGetErrorString(e));
+}

@@ -42,6 +42,14 @@ _SIGNATURES = {
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "dllm_fork_layout": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "dllm_rmsnorm_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_float,
+                                  _c_int, _c_int, _c_int, _c_void_p]),
+    "dllm_gated_rmsnorm_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_float, _c_int,
+                                        _c_int, _c_void_p]),
+    "dllm_swiglu_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p]),
+    "dllm_qk_norm_rope_fwd": (_c_int, [
+        _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p]),
     "dllm_bd_attention_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p]),

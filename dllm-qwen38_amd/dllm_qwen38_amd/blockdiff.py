@@ -21,9 +21,11 @@ Per layer:
     both halves), then the complementary-mask attention kernel, which derives visibility from
     (L, block) and skips hidden tiles (no [2L, 2L] mask exists), then the sigmoid output gate and
     o_proj.
-The GEMMs, norms, RoPE and gates run as torch ops on the same stream; the mixers are the HIP
-kernels of libdllm_hip.so. Forward only: the HIP ops have no backward, so a call that would need
-gradients raises instead of returning a graph that silently stops at the kernels.
+The GEMMs (hipBLASLt through torch) and the sigmoid output gate run as torch ops on the same
+stream; the mixers, the norms (each residual add fused into the norm after it), the SwiGLU product
+and the q/k norm + RoPE prologue are HIP kernels of libdllm_hip.so. Forward only: the HIP ops have
+no backward, so a call that would need gradients raises instead of returning a graph that
+silently stops at the kernels.
 """
 
 from __future__ import annotations
@@ -34,7 +36,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from . import attention, gdn
+from . import attention, gdn, norms
 from .attention import block_causal_mask, complementary_mask  # noqa: F401  (re-exported, reference names)
 
 FULL = "full_attention"
@@ -67,24 +69,15 @@ def _eps(norm) -> float:
     return float(getattr(norm, "eps", getattr(norm, "variance_epsilon", 1e-6)))
 
 
-def rmsnorm(x: torch.Tensor, norm) -> torch.Tensor:
-    """Qwen3.5 RMSNorm: fp32 normalisation, weight applied as (1 + w), cast back ([hf]:720-737)."""
-    xf = x.float()
-    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + _eps(norm))
-    return (y * (1.0 + norm.weight.float())).type_as(x)
-
-
-def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, norm) -> torch.Tensor:
-    """rmsnorm(x) * w * silu(z): norm in fp32, weight product in x's dtype ([hf]:168-184)."""
-    dt = x.dtype
-    xf = x.float()
-    y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + _eps(norm))).to(dt)
-    return (norm.weight * y * F.silu(z.float())).to(dt)
+def rmsnorm(x: torch.Tensor, norm, residual: torch.Tensor | None = None):
+    """Qwen3.5 RMSNorm with (1 + w) ([hf]:720-737) on the HIP kernel; with a residual, returns
+    (norm(x + residual), x + residual) from one pass."""
+    return norms.rmsnorm(x, norm.weight, _eps(norm), residual=residual)
 
 
 def mlp(m, x: torch.Tensor) -> torch.Tensor:
-    """SwiGLU ([hf]:704-717)."""
-    return m.down_proj(F.silu(m.gate_proj(x)) * m.up_proj(x))
+    """SwiGLU ([hf]:704-717): the two projections, one fused silu-product kernel, the down projection."""
+    return m.down_proj(norms.swiglu(m.gate_proj(x), m.up_proj(x)))
 
 
 def rotary_tables(text_model, L: int, device, dtype):
@@ -95,17 +88,6 @@ def rotary_tables(text_model, L: int, device, dtype):
     emb = torch.cat([fr, fr], -1)
     scale = float(getattr(text_model.rotary_emb, "attention_scaling", 1.0))
     return (emb.cos() * scale).to(dtype), (emb.sin() * scale).to(dtype)
-
-
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Partial RoPE on the first rotary_dim dims of x [B, S, H, d] with tables [S, rotary_dim]
-    ([hf]:554-589)."""
-    rd = cos.shape[-1]
-    xr, xp = x[..., :rd], x[..., rd:]
-    c, s = cos[:, None, :], sin[:, None, :]
-    half = rd // 2
-    rot = torch.cat([-xr[..., half:], xr[..., :half]], -1)
-    return torch.cat([xr * c + rot * s, xp], -1)
 
 
 def _gdn_fork_arm(m, n0: torch.Tensor, nt: torch.Tensor, block: int, fault: BreakMode):
@@ -125,45 +107,50 @@ def _gdn_fork_arm(m, n0: torch.Tensor, nt: torch.Tensor, block: int, fault: Brea
                        block=block, conv_bias=m.conv1d.bias, need_states=False, need_tails=False,
                        fault="no-conv-prefix" if fault.drop_conv_prefix else None,
                        out={"ot": core[:B], "o0": core[B:]})
-    o = gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm).reshape(2 * B, L, -1)
+    o = norms.gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm.weight, _eps(m.norm)).reshape(2 * B, L, -1)
     out = m.out_proj(o)
     return out[B:], out[:B]
 
 
 def _attention_arm(att, n0: torch.Tensor, nt: torch.Tensor, cos, sin, block: int, fault: BreakMode):
-    """FULL arm (blockdiff.py:178-182 through [hf]:656-701) on cat([x_t, x_0])."""
+    """FULL arm (blockdiff.py:178-182 through [hf]:656-701) on cat([x_t, x_0]). cos/sin: rotary
+    tables [L, rotary_dim] for positions 0..L-1, shared by both halves."""
     B, L, _ = n0.shape
     x = torch.cat([nt, n0], 1)  # [B, 2L, D]
     S = 2 * L
     hd = att.head_dim
     q, gate = torch.chunk(att.q_proj(x).view(B, S, -1, 2 * hd), 2, dim=-1)
     gate = gate.reshape(B, S, -1)
-    q = rmsnorm(q, att.q_norm)
-    k = rmsnorm(att.k_proj(x).view(B, S, -1, hd), att.k_norm)
+    q, k = norms.qk_norm_rope(q, att.k_proj(x).view(B, S, -1, hd), att.q_norm, att.k_norm, cos, sin, L)
     v = att.v_proj(x).view(B, S, -1, hd)
-    q = apply_rope(q, cos, sin)
-    k = apply_rope(k, cos, sin)
     o = attention.bd_attention(q, k, v, block=block, scale=float(att.scaling), leak_xt_prefix=fault.leak_xt_prefix)
     out = att.o_proj(o.reshape(B, S, -1) * torch.sigmoid(gate))
     return out[:, L:], out[:, :L]
 
 
-def layer_step(layer, kind: str, h0: torch.Tensor, ht: torch.Tensor, *, block: int, cos2, sin2,
-               fault: BreakMode | None = None):
-    """One decoder layer for both streams (blockdiff.py:147-188). cos2/sin2: rotary tables
-    [2L, rotary_dim] for cat([x_t, x_0]) (positions shared by the halves)."""
+def layer_step(layer, kind: str, h0: torch.Tensor, ht: torch.Tensor, *, block: int, cos, sin,
+               fault: BreakMode | None = None, m0: torch.Tensor | None = None, mt: torch.Tensor | None = None):
+    """One decoder layer for both streams (blockdiff.py:147-188). cos/sin: rotary tables
+    [L, rotary_dim] (positions shared by the halves of cat([x_t, x_0])).
+
+    m0/mt: the previous layer's MLP outputs not yet added to h0/ht (None: nothing pending); their
+    residual add is fused into this layer's input norm. Returns (h0, ht, m0, mt): the streams
+    after the mixer residual and this layer's MLP outputs, again pending."""
     fault = fault or BreakMode()
-    n0, nt = rmsnorm(h0, layer.input_layernorm), rmsnorm(ht, layer.input_layernorm)
+    if m0 is None:
+        n0, nt = rmsnorm(h0, layer.input_layernorm), rmsnorm(ht, layer.input_layernorm)
+    else:
+        n0, h0 = rmsnorm(m0, layer.input_layernorm, residual=h0)
+        nt, ht = rmsnorm(mt, layer.input_layernorm, residual=ht)
     if kind == LINEAR:
         o0, ot = _gdn_fork_arm(layer.linear_attn, n0, nt, block, fault)
     elif kind == FULL:
-        o0, ot = _attention_arm(layer.self_attn, n0, nt, cos2, sin2, block, fault)
+        o0, ot = _attention_arm(layer.self_attn, n0, nt, cos, sin, block, fault)
     else:
         raise ValueError(f"unknown layer type {kind}")
-    h0, ht = h0 + o0, ht + ot
-    h0 = h0 + mlp(layer.mlp, rmsnorm(h0, layer.post_attention_layernorm))
-    ht = ht + mlp(layer.mlp, rmsnorm(ht, layer.post_attention_layernorm))
-    return h0, ht
+    n0, h0 = rmsnorm(o0, layer.post_attention_layernorm, residual=h0)
+    nt, ht = rmsnorm(ot, layer.post_attention_layernorm, residual=ht)
+    return h0, ht, mlp(layer.mlp, n0), mlp(layer.mlp, nt)
 
 
 def _forbid_grad(*modules):
@@ -197,12 +184,15 @@ def block_diffusion_forward(text_model, lm_head, x0_ids: torch.Tensor, xt_ids: t
     h0 = text_model.embed_tokens(x0_ids)
     ht = text_model.embed_tokens(xt_ids)
     cos, sin = rotary_tables(text_model, L, h0.device, h0.dtype)
-    cos2, sin2 = torch.cat([cos, cos], 0), torch.cat([sin, sin], 0)
     n = cfg.num_hidden_layers if layers is None else layers
+    m0 = mt = None
     for i in range(n):
-        h0, ht = layer_step(text_model.layers[i], cfg.layer_types[i], h0, ht, block=block, cos2=cos2, sin2=sin2,
-                            fault=fault)
-    ht, h0 = rmsnorm(ht, text_model.norm), rmsnorm(h0, text_model.norm)
+        h0, ht, m0, mt = layer_step(text_model.layers[i], cfg.layer_types[i], h0, ht, block=block, cos=cos, sin=sin,
+                                    fault=fault, m0=m0, mt=mt)
+    if m0 is None:
+        ht, h0 = rmsnorm(ht, text_model.norm), rmsnorm(h0, text_model.norm)
+    else:
+        ht, h0 = rmsnorm(mt, text_model.norm, residual=ht)[0], rmsnorm(m0, text_model.norm, residual=h0)[0]
     if output == "hidden":
         return ht, h0
     return lm_head(ht), lm_head(h0)
@@ -227,10 +217,11 @@ class LayerStep(nn.Module):
             raise ValueError("LayerStep takes no dense attention mask: visibility is derived from block")
         _forbid_grad(self.layer)
         cos, sin = pos
-        S = 2 * h0.shape[1]
-        cos2 = cos.reshape(-1, S, cos.shape[-1])[0].to(h0.dtype)
-        sin2 = sin.reshape(-1, S, sin.shape[-1])[0].to(h0.dtype)
-        return layer_step(self.layer, self.kind, h0, ht, block=block, cos2=cos2, sin2=sin2, fault=self.fault)
+        L = h0.shape[1]
+        cos1 = cos.reshape(-1, 2 * L, cos.shape[-1])[0, :L].to(h0.dtype)  # both halves share positions
+        sin1 = sin.reshape(-1, 2 * L, sin.shape[-1])[0, :L].to(h0.dtype)
+        h0, ht, m0, mt = layer_step(self.layer, self.kind, h0, ht, block=block, cos=cos1, sin=sin1, fault=self.fault)
+        return h0 + m0, ht + mt
 
 
 @torch.no_grad()

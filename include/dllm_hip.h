@@ -123,6 +123,46 @@ int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, const void* k
                           const void* v, const int64_t* v_strides, void* out, int B, int L, int Hq, int Hkv,
                           int d, int block, float scale, int dtype, int flags, void* stream);
 
+/*
+ * Qwen3.5 RMSNorm over the last dim of x [rows, dim]: y = x * rsqrt(mean(x^2) + eps) * (1 + w)
+ * in fp32 (unit_offset = 1; 0 applies w as is), rounded once to x's dtype.
+ * Replaces [hf]:720-737 Qwen3_5RMSNorm as called by the decoder layer and the final norm
+ * (src/dllm_qwen38/blockdiff.py:150,186-187,200). With residual != NULL the normed value is
+ * s = x + residual rounded to x's dtype (the residual adds of [hf]:785,791), and s is also written
+ * to sum_out when that is non-NULL. All tensors contiguous; weight [dim].
+ */
+int dllm_rmsnorm_fwd(const void* x, const void* residual, void* sum_out, const void* weight, void* y,
+                     int rows, int dim, float eps, int dtype, int dtype_w, int unit_offset, void* stream);
+
+/*
+ * Gated RMSNorm of the GDN output: y = round(w * round(rmsnorm(x))) * silu(z), rounded to x's dtype.
+ * Replaces [hf]:168-184 Qwen3_5RMSNormGated as called at src/dllm_qwen38/gdn.py:232.
+ * x, z [rows, dim] contiguous; weight [dim].
+ */
+int dllm_gated_rmsnorm_fwd(const void* x, const void* z, const void* weight, void* y, int rows, int dim,
+                           float eps, int dtype, int dtype_w, void* stream);
+
+/*
+ * SwiGLU product of the MLP: out = round(round(silu(gate)) * up), n elements, 16-byte aligned.
+ * Replaces the act_fn(gate_proj(x)) * up_proj(x) of [hf]:704-717.
+ */
+int dllm_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/*
+ * Attention prologue: per (token, head) row of q [B,S,Hq,hd] and k [B,S,Hkv,hd] (strides {b,t,h}
+ * in elements, last dim contiguous): RMSNorm over hd with (1 + w), then partial RoPE on the first
+ * rotary_dim dims, out = a*cos + rotate_half(a)*sin with products and sum rounded to the dtype.
+ * Token t reads table row t mod L (positions shared by both halves of cat([x_t, x_0]),
+ * src/dllm_qwen38/blockdiff.py:143-144). cos/sin [L, rotary_dim] in the activation dtype.
+ * Writes contiguous q_out [B,S,Hq,hd], k_out [B,S,Hkv,hd]. hd <= 256.
+ * Replaces [hf]:672-680 (q_norm, k_norm, apply_rotary_pos_emb [hf]:554-589).
+ */
+int dllm_qk_norm_rope_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                          const void* q_norm_w, const void* k_norm_w, const void* cos_table,
+                          const void* sin_table, void* q_out, void* k_out, int B, int S, int L, int Hq,
+                          int Hkv, int head_dim, int rotary_dim, float eps, int dtype, int dtype_w,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,13 +8,17 @@
 // every SIMD runs one clean and one noised wave and each hides the other's latency).
 // Per tile and stream:
 //   load    q, k (key head hv / (Hv/Hk): GQA by indexing, no expansion), v, beta, g from the
-//           registers prefetched during the previous tile; l2norm (DPP reductions) and Dk^-1/2 in
-//           fp32; gamma = sequential cumsum of g; operands into LDS.
-//   G       K^K^T and Q^K^T on MFMA; decay/beta masks -> A (fp32), P.
-//   T       T = (I + A)^-1 in fp32 by a blocked inverse (8x8 diagonal blocks by forward
-//           substitution, then 8x8 and 16x16 off-diagonal blocks by products) inside the wave
-//           that produced A; T1 = T diag(beta e^gamma), T2 = T diag(beta).
-//   W       W = T1 K^ (= (I+A)^-1 (beta K^ e^gamma)) on MFMA, written over K^.
+//           registers prefetched during the previous tile, raw into LDS (bf16: all row-major;
+//           the transposed operands come from LDS transpose reads); q row norms (DPP
+//           reductions); gamma = inclusive scan of g over the tile (DPP).
+//   G       K K^T and Q K^T on MFMA (k norms from the Gram diagonal); decay/beta masks -> A
+//           (fp32), P with the q norms and Dk^-1/2 folded in.
+//   T       T = (I + A)^-1 in fp32 by a blocked inverse inside the wave that produced A: 8x8
+//           diagonal blocks by forward substitution, then the 8x8 and the 16x16 off-diagonal
+//           blocks by products. The MFMA operands T1 = T diag(beta e^gamma / ||k||) and
+//           T2 = T diag(beta) are formed from it in registers where they are used.
+//   W       W = T1 K (= (I+A)^-1 (beta K^ e^gamma)) on MFMA (bf16: into its own rows; fp32:
+//           written over the raw k rows).
 //   state   wave u of the clean set: U = T2 V, V' = U - W S, O = e^gamma (Q^ S) + P V',
 //           S <- e^gamma_last S + K^T (e^(gamma_last - gamma) V'), snapshot S every chunk;
 //           wave u of the noised set: the same O with the noised tile's operands and the clean
@@ -71,6 +75,11 @@ __device__ __forceinline__ int opaque_v(int x) {
   return x;
 }
 
+// DPP move; lanes whose source is outside the row read 0 (bound_ctrl).
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
 // Sum over each aligned group of 8 lanes, returned to all 8 (DPP: no LDS round trip). The three
 // steps are quad_perm [1,0,3,2], quad_perm [2,3,0,1] and row_half_mirror.
 __device__ __forceinline__ float dpp_sum8(float x) {
@@ -93,14 +102,12 @@ struct GdnSmem {
   static constexpr int O_KT = O_KH + 32 * QROW * (int)sizeof(OpT);
   static constexpr int O_VT = O_KT + DK * TROW * (int)sizeof(OpT);
   static constexpr int O_P = O_VT + DVW * TROW * (int)sizeof(OpT);
-  static constexpr int O_T1 = O_P + 32 * TROW * (int)sizeof(OpT);
-  static constexpr int O_T2 = O_T1 + 32 * TROW * (int)sizeof(OpT);
-  static constexpr int O_AF = O_T2 + 32 * TROW * (int)sizeof(OpT);
+  static constexpr int O_AF = O_P + 32 * TROW * (int)sizeof(OpT);
   static constexpr int FROW = 36;  // fp32 [32][32] scratch row stride (16-byte aligned rows)
   static constexpr int O_TF = O_AF + 32 * FROW * 4;
   static constexpr int O_YF = O_TF + 32 * FROW * 4;
-  static constexpr int O_VEC = O_YF + 16 * 20 * 4;  // eight per-row vectors of 32 floats
-  static constexpr int STREAM_BYTES = ((O_VEC + 8 * 32 * 4) + 15) & ~15;
+  static constexpr int O_VEC = O_YF + 16 * 20 * 4;  // nine per-row vectors of 32 floats
+  static constexpr int STREAM_BYTES = ((O_VEC + 9 * 32 * 4) + 15) & ~15;
   // bf16 keeps k and v row-major (transposed operands come from LDS transpose reads): the two
   // transposed regions hold W rows [32][QROW] and v rows [32][VROW] instead
   static constexpr int VROW = DVW + 8;
@@ -189,8 +196,6 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
   OpT* const VH = VT;                          // bf16: raw v rows       [32][VROW]
   constexpr int VROW = SM::VROW;
   OpT* const PP = (OpT*)(sbase + SM::O_P);     // P with q row norms    [32][32]
-  OpT* const T1 = (OpT*)(sbase + SM::O_T1);    // T diag(beta e^g rnk)  [32][32]
-  OpT* const T2 = (OpT*)(sbase + SM::O_T2);    // T diag(beta)          [32][32]
   float* const AF = (float*)(sbase + SM::O_AF);
   float* const TF = (float*)(sbase + SM::O_TF);
   float* const YF = (float*)(sbase + SM::O_YF);
@@ -202,6 +207,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
   float* const RNQ = GAML + 160;                    // scale/||q||
   float* const EGQ = GAML + 192;                    // e^gamma scale/||q||
   float* const EGLK = GAML + 224;                   // e^(gamma_last - gamma)/||k||
+  float* const BER = GAML + 256;                    // beta e^gamma/||k|| (column scale of T1)
   auto SBUF = [&](int sl, int kt) { return (F*)(smem + SM::O_SB) + ((sl * KT + kt) * 64 + lane); };
 
   // this set's stream: base pointers at (b, head)
@@ -339,21 +345,18 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
       }
       ss = dpp_sum8(ss);
       if (lseg == 0) RNQ[lr] = a.l2norm ? a.scale * rsqrtf(ss + 1e-6f) : a.scale;
-      // beta, g and the cumulative decay in sequential order (as a cumsum), one wave per set
+      // beta, g and the cumulative decay (inclusive scan over the tile's rows), one wave per set:
+      // lanes 0..31 hold g of rows 0..31 (zero for padding rows and for lanes 32..63); scan
+      // within each 16-lane DPP row, then carry row 0's total into row 1 (row_bcast:15)
       if (u == 0) {
-        if (h == 0) GAML[l32] = rg;
-        wave_lds_sync();
-        float gam = 0.f, gall = 0.f;
-#pragma unroll
-        for (int q = 0; q < 32; q += 4) {
-          const f32x4 g4 = *(const f32x4*)(GAML + q);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (q + e <= lo) gam += g4[e];
-            gall += g4[e];
-          }
-        }
-        wave_lds_sync();
+        float x = rg;
+        x += dpp_mov<0x111>(x);  // row_shr:1
+        x += dpp_mov<0x112>(x);  // row_shr:2
+        x += dpp_mov<0x114>(x);  // row_shr:4
+        x += dpp_mov<0x118>(x);  // row_shr:8
+        x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
+        const float gam = x;
+        const float gall = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 31));
         if (h == 0) {
           GAML[l32] = gam * LOG2E;
           BET[l32] = rb;
@@ -503,6 +506,36 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
               TF[(8 * (m + 1) + ii) * FROW + 8 * m + jj] = -sacc;
             }
           }
+          wave_lds_sync();
+          // level 2 (this wave): T[16:32][0:16] = -T22 (A21 T11), lane -> row 16 + i2, columns j2..j2+3;
+          // every other entry of the lower triangle is final in TF after levels 0 and 1
+          {
+            const int i2 = lane >> 2, j2 = (lane & 3) * 4;
+            f32x4 arow[4], tcol[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) arow[q] = *(const f32x4*)(AF + (16 + i2) * FROW + 4 * q);
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) tcol[kk] = *(const f32x4*)(TF + kk * FROW + j2);
+            f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) y[e] = __builtin_fmaf(arow[kk >> 2][kk & 3], tcol[kk][e], y[e]);
+            *(f32x4*)(YF + i2 * 20 + j2) = y;
+            wave_lds_sync();
+            f32x4 trow[4], ycol[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) trow[q] = *(const f32x4*)(TF + (16 + i2) * FROW + 16 + 4 * q);
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) ycol[kk] = *(const f32x4*)(YF + kk * 20 + j2);
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(trow[kk >> 2][kk & 3], ycol[kk][e], z[e]);
+            *(f32x4*)(TF + (16 + i2) * FROW + j2) = -z;
+          }
+          if (h == 0) BER[l32] = BET[l32] * EG[l32] * RNK[l32];
         } else {
           f32x4 rnq4[4];
 #pragma unroll
@@ -522,63 +555,25 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
     }
     __syncthreads();
 
-    // ------------------------------------------------------------------ T level 2 (all waves of the set)
-    // T[16:32][0:16] = -T16_1 (A[16:32][0:16] T16_0); the final entries elsewhere are already in TF.
-    // Thread ts owns entry (ii, jj) of the 16x16 block and writes the scaled operand copies
-    // T1 = T diag(beta e^gamma / ||k||) and T2 = T diag(beta) for four entries.
-    const int tso = opaque_v(ts);
-    const int ii = tso >> 4, jj = tso & 15;
-    {
-      f32x4 arow[4];
-      float tcol[16];
+    // T operand fragments, built from the fp32 T (lower triangle, diagonal included) with a
+    // per-column scale: lane = row l32, columns rho(v, h)
+    auto t_frag = [&](const float* colscale, F& f) {
+      f32x16 tv;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) arow[q] = *(const f32x4*)(AF + (16 + ii) * FROW + 4 * q);
+      for (int m = 0; m < 4; ++m) {
+        const f32x4 t4 = *(const f32x4*)(TF + l32 * FROW + 8 * m + 4 * h);
+        const f32x4 c4 = *(const f32x4*)(colscale + 8 * m + 4 * h);
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk) tcol[kk] = TF[kk * FROW + jj];
-      // rows 0..15 (all columns) and the T16_1 block are final: scaled copies now
-      const int i0 = tso >> 4, j0 = (tso & 15) * 2;  // rows 0..15, columns j0, j0+1
-      const int i1 = 16 + (tso >> 4), j1 = 16 + (tso & 15);  // T16_1 block
-      const f32x2 t0v = *(const f32x2*)(TF + i0 * FROW + j0);
-      const float t1v = TF[i1 * FROW + j1];
-      const f32x2 b0 = *(const f32x2*)(BET + j0), e0 = *(const f32x2*)(EG + j0), r0 = *(const f32x2*)(RNK + j0);
-      const float b1 = BET[j1], e1 = EG[j1], r1 = RNK[j1];
-      float y = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) y = __builtin_fmaf(arow[kk >> 2][kk & 3], tcol[kk], y);
-      YF[ii * 20 + jj] = y;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float tv = (j0 + e <= i0) ? t0v[e] : 0.f;
-        T1[i0 * TROW + j0 + e] = from_f32<OpT>(tv * (b0[e] * e0[e] * r0[e]));
-        T2[i0 * TROW + j0 + e] = from_f32<OpT>(tv * b0[e]);
+        for (int e = 0; e < 4; ++e) tv[4 * m + e] = (8 * m + 4 * ho + e <= lo) ? t4[e] * c4[e] : 0.f;
       }
-      const float tv1 = (j1 <= i1) ? t1v : 0.f;
-      T1[i1 * TROW + j1] = from_f32<OpT>(tv1 * (b1 * e1 * r1));
-      T2[i1 * TROW + j1] = from_f32<OpT>(tv1 * b1);
-    }
-    __syncthreads();
-    {
-      f32x4 trow[4];
-      float ycol[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) trow[q] = *(const f32x4*)(TF + (16 + ii) * FROW + 16 + 4 * q);
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) ycol[kk] = YF[kk * 20 + jj];
-      const float bj = BET[jj], ej = EG[jj], rj = RNK[jj];
-      float z = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 16; ++kk) z = __builtin_fmaf(trow[kk >> 2][kk & 3], ycol[kk], z);
-      const float tv = -z;
-      T1[(16 + ii) * TROW + jj] = from_f32<OpT>(tv * (bj * ej * rj));
-      T2[(16 + ii) * TROW + jj] = from_f32<OpT>(tv * bj);
-    }
-    __syncthreads();
+      acc_to_frag(tv, f);
+    };
 
     // ------------------------------------------------------------------ W phase: W = T1 K_raw
     if (u < KT) {
       const int kt = u;
       F fa, fb;
-      lds_frag(T1 + l32 * TROW, h, fa);
+      t_frag(BER, fa);  // T1 = T diag(beta e^gamma / ||k||)
       if constexpr (BF16) {
         lds_frag_tr(KH + kt * 32, QROW, lane, fb);
       } else {
@@ -598,7 +593,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
       f32x16 accU = zero16(), accWS = zero16(), accQS = zero16();
       {
         F fa, fb;
-        lds_frag(T2 + l32 * TROW, h, fa);
+        t_frag(BET, fa);  // T2 = T diag(beta)
         if constexpr (BF16) {
           lds_frag_tr(VH + u * 32, VROW, lane, fb);
         } else {

@@ -20,6 +20,12 @@
 // come from gfx950 LDS transpose reads), the next tile's global loads travelling during the current
 // compute.
 // GQA: query head h reads KV head h / (Hq / Hkv), no repeat_kv copy.
+//
+// Block-causal mode (template flag BC): one sequence of N keys at absolute positions 0..N-1 (a
+// cached clean prefix plus the current segment) and M query rows at absolute positions q0..q0+M-1;
+// query i sees key j iff j / C <= (q0 + i) / C. It is the x_0 -> x_0 rule above with the query rows
+// offset, so the kernels run it as half 1 with its own row counts: a decode step (M = C, q0 = N - C,
+// every key visible) and the prefill of a prompt (q0 = 0, M = N) are both this mode.
 #include <type_traits>
 
 #include "common.h"
@@ -35,6 +41,7 @@ struct AttnArgs {
   int q_st, q_sh, k_st, k_sh, v_st, v_sh;
   int B, L, Hq, Hkv, d, C;
   int leak;
+  int M, N, q0;       // block-causal mode: query rows, key rows, absolute position of query row 0
   float scale_log2e;  // softmax scale * log2(e)
   int vec;            // 16-byte vector loads of q/k/v rows allowed
 };
@@ -80,7 +87,7 @@ struct AttnSmem {
   static constexpr int TOTAL = 2 * STAGE;
 };
 
-template <int D, bool BF16>
+template <int D, bool BF16, bool BC>
 __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
   using SM = AttnSmem<D, BF16>;
   using OpT = typename SM::OpT;
@@ -97,17 +104,21 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int L = a.L, C = a.C;
-  const int ntq = (L + 31) >> 5;  // 32-row tiles per half
+  const int Lq = BC ? a.M : L;     // query rows per half
+  const int Lk = BC ? a.N : L;     // key rows per half
+  const int qa = BC ? a.q0 : 0;    // absolute position of query row 0
+  const int ntq = (Lq + 31) >> 5;  // 32-row tiles per half
   const int ng = (ntq + 3) >> 2;  // groups of four tiles per half
   const int rep = a.Hq / a.Hkv;
 
   // work unit: longest first (tile group descending), then half, batch, KV head, query head in group
   const int lin = xcd_linear_id_attn(blockIdx.x, gridDim.x);
-  const int per_g = 2 * a.B * a.Hkv * rep;
+  constexpr int NH = BC ? 1 : 2;  // query halves
+  const int per_g = NH * a.B * a.Hkv * rep;
   const int g = ng - 1 - lin / per_g;
   int rem = lin % per_g;
-  const int qh = rem % 2;  // alternate halves so equal-work units sit together
-  rem /= 2;
+  const int qh = BC ? 1 : rem % 2;  // alternate halves so equal-work units sit together
+  rem /= NH;
   const int hr = rem % rep;
   rem /= rep;
   const int hkv = rem % a.Hkv;
@@ -115,18 +126,18 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
   const int hq = hkv * rep + hr;
 
   // this wave's query rows [r0, r1) inside half qh; the workgroup's rows [g0, g1)
-  const int g0 = g * 128, g1 = min(L, g0 + 128);
-  const int r0 = g0 + wave * 32, r1 = min(L, r0 + 32);
-  const bool wave_live = r0 < L;
-  const int qb0 = r0 / C, qb1 = (max(r0, r1 - 1)) / C;
-  const int gqb0 = g0 / C, gqb1 = (g1 - 1) / C;
+  const int g0 = g * 128, g1 = min(Lq, g0 + 128);
+  const int r0 = g0 + wave * 32, r1 = min(Lq, r0 + 32);
+  const bool wave_live = r0 < Lq;
+  const int qb0 = (qa + r0) / C, qb1 = (qa + max(r0, r1 - 1)) / C;
+  const int gqb0 = (qa + g0) / C, gqb1 = (qa + g1 - 1) / C;
 
   // key ranges of the workgroup, per half: [lo, hi) in tokens
   int lo0, hi0, lo1, hi1;  // half 0 (x_t) and half 1 (x_0)
   if (qh == 1) {
     lo0 = hi0 = 0;
     lo1 = 0;
-    hi1 = min(L, (gqb1 + 1) * C);
+    hi1 = min(Lk, (gqb1 + 1) * C);
   } else {
     lo0 = a.leak ? 0 : gqb0 * C;
     hi0 = min(L, (gqb1 + 1) * C);
@@ -150,8 +161,8 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
   // Q^T fragments for this wave's 32 queries (lane = query, d in rho order), kept in registers
   F qf[DT];
   {
-    const int row = min(r0 + l32, L - 1);  // rows past L load a valid row and are never stored
-    const OpT* qp = qbase + (long long)(qh * L + row) * a.q_st;
+    const int row = min(r0 + l32, Lq - 1);  // rows past the end load a valid row and are never stored
+    const OpT* qp = qbase + (long long)((BC ? 0 : qh * L) + row) * a.q_st;
 #pragma unroll
     for (int s = 0; s < DT; ++s) {
       if constexpr (BF16) {
@@ -182,8 +193,8 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
     int kh, j0;
     tile_pos(n, kh, j0);
     const int key = j0 + kr;
-    const bool ok = key < L;
-    const int krow = kh * L + (ok ? key : 0);
+    const bool ok = key < Lk;
+    const int krow = (BC ? 0 : kh * L) + (ok ? key : 0);
     const OpT* kp = kbase + (long long)krow * a.k_st;
     const OpT* vp = vbase + (long long)krow * a.v_st;
 #pragma unroll
@@ -205,7 +216,7 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
   auto store_tile = [&](int n, int stage) {
     int kh, j0;
     tile_pos(n, kh, j0);
-    const bool ok = j0 + kr < L;
+    const bool ok = j0 + kr < Lk;
     OpT* Ks = (OpT*)(smem + stage * SM::STAGE);
     OpT* Vs = (OpT*)(smem + stage * SM::STAGE + SM::K_BYTES);
 #pragma unroll
@@ -238,10 +249,10 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
     if (n + 1 < ntiles) load_tile(n + 1);
     int kh, j0;
     tile_pos(n, kh, j0);
-    const int kb0 = j0 / C, kb1 = (min(L, j0 + 32) - 1) / C;
+    const int kb0 = j0 / C, kb1 = (min(Lk, j0 + 32) - 1) / C;
     bool any = false, all = false;
     if (wave_live) classify(qh, qb0, qb1, kh, kb0, kb1, a.leak, any, all);
-    const bool ragged = (j0 + 32 > L) || (r1 - r0 < 32);
+    const bool ragged = (j0 + 32 > Lk) || (r1 - r0 < 32);
     if (any) {
       const OpT* Ks = (const OpT*)(smem + (n & 1) * SM::STAGE);
       const OpT* Vs = (const OpT*)(smem + (n & 1) * SM::STAGE + SM::K_BYTES);
@@ -260,11 +271,11 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
       for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;
       if (!all || ragged) {
         const int qi = r0 + l32;
-        const int qbl = qi / C;
+        const int qbl = (qa + qi) / C;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int kj = j0 + rho(v, h);
-          const bool okk = kj < L && qi < L && visible(qh, qbl, kh, kj / C, a.leak);
+          const bool okk = kj < Lk && qi < Lq && visible(qh, qbl, kh, kj / C, a.leak);
           st[v] = okk ? st[v] : -INFINITY;
         }
       }
@@ -321,9 +332,10 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
 
   // O = (O^T)^T / l : lane = query row, four runs of four consecutive d per 32-slice
   const int qi = r0 + l32;
-  if (wave_live && qi < L) {
+  if (wave_live && qi < Lq) {
     const float inv = 1.f / lrow;
-    OpT* op = (OpT*)a.out + (((long long)b * 2 * L + qh * L + qi) * a.Hq + hq) * a.d;
+    const long long orow = BC ? (long long)b * Lq + qi : (long long)b * 2 * L + qh * L + qi;
+    OpT* op = (OpT*)a.out + (orow * a.Hq + hq) * a.d;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
@@ -345,13 +357,13 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
   }
 }
 
-template <int D, bool BF16>
+template <int D, bool BF16, bool BC>
 static int launch_attn(const AttnArgs& a, hipStream_t st) {
-  const int ntq = (a.L + 31) / 32;
+  const int ntq = ((BC ? a.M : a.L) + 31) / 32;
   const int ng = (ntq + 3) / 4;
-  const long long nblk = (long long)ng * 2 * a.B * a.Hq;
+  const long long nblk = (long long)ng * (BC ? 1 : 2) * a.B * a.Hq;
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "attention: grid too large");
-  bd_attn_kernel<D, BF16><<<dim3((unsigned)nblk), dim3(256), 0, st>>>(a);
+  bd_attn_kernel<D, BF16, BC><<<dim3((unsigned)nblk), dim3(256), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention launch: %s", hipGetErrorString(e));
   return DLLM_OK;
@@ -389,7 +401,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-template <int D>
+template <int D, bool BC>
 __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   using SM = DmaSmem<D>;
   using F = Frag<true>;
@@ -410,32 +422,36 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int pair = wave >> 1, e = wave & 1;
   const int L = a.L, C = a.C;
-  const int ntq = (L + 31) >> 5;
+  const int Lq = BC ? a.M : L;
+  const int Lk = BC ? a.N : L;
+  const int qa = BC ? a.q0 : 0;
+  const int ntq = (Lq + 31) >> 5;
   const int ng = (ntq + 3) >> 2;
   const int rep = a.Hq / a.Hkv;
 
   const int lin = xcd_linear_id_attn(blockIdx.x, gridDim.x);
-  const int per_g = 2 * a.B * a.Hkv * rep;
+  constexpr int NH = BC ? 1 : 2;
+  const int per_g = NH * a.B * a.Hkv * rep;
   const int g = ng - 1 - lin / per_g;
   int rem = lin % per_g;
-  const int qh = rem % 2;
-  rem /= 2;
+  const int qh = BC ? 1 : rem % 2;
+  rem /= NH;
   const int hr = rem % rep;
   rem /= rep;
   const int hkv = rem % a.Hkv;
   const int b = rem / a.Hkv;
   const int hq = hkv * rep + hr;
 
-  const int g0 = g * 128, g1 = min(L, g0 + 128);
-  const int r0 = g0 + pair * 32, r1 = min(L, r0 + 32);
-  const bool wave_live = r0 < L;
-  const int qb0 = r0 / C, qb1 = (max(r0, r1 - 1)) / C;
-  const int gqb0 = g0 / C, gqb1 = (g1 - 1) / C;
+  const int g0 = g * 128, g1 = min(Lq, g0 + 128);
+  const int r0 = g0 + pair * 32, r1 = min(Lq, r0 + 32);
+  const bool wave_live = r0 < Lq;
+  const int qb0 = (qa + r0) / C, qb1 = (qa + max(r0, r1 - 1)) / C;
+  const int gqb0 = (qa + g0) / C, gqb1 = (qa + g1 - 1) / C;
   int lo0, hi0, lo1, hi1;
   if (qh == 1) {
     lo0 = hi0 = 0;
     lo1 = 0;
-    hi1 = min(L, (gqb1 + 1) * C);
+    hi1 = min(Lk, (gqb1 + 1) * C);
   } else {
     lo0 = a.leak ? 0 : gqb0 * C;
     hi0 = min(L, (gqb1 + 1) * C);
@@ -461,8 +477,8 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   // d = 32s + 8h .. +7, the second 32s + 16 + 8h .. +7 (16-byte loads, 16-byte LDS reads).
   F qf[DT];
   {
-    const int row = min(r0 + l32, L - 1);
-    const bf16* qp = qbase + (long long)(qh * L + row) * a.q_st;
+    const int row = min(r0 + l32, Lq - 1);
+    const bf16* qp = qbase + (long long)((BC ? 0 : qh * L) + row) * a.q_st;
 #pragma unroll
     for (int s = 0; s < DT; ++s) {
       qf[s].lo = *(const bf16x8*)(qp + 32 * s + 8 * h);
@@ -483,8 +499,8 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
       const int row0 = (gi % IPT) * RPI;
       const int row = row0 + lane / CH;
       const int chunk = (lane % CH) ^ (row & (CH - 1));
-      const int key = min(j0 + row, L - 1);  // rows past L load a valid row; they are masked
-      const long long off = (long long)(kh * L + key) * (isv ? a.v_st : a.k_st) + chunk * 8;
+      const int key = min(j0 + row, Lk - 1);  // rows past the end load a valid row; they are masked
+      const long long off = (long long)((BC ? 0 : kh * L) + key) * (isv ? a.v_st : a.k_st) + chunk * 8;
       const bf16* src = (isv ? vbase : kbase) + off;
       unsigned char* dst = sb + (isv ? SM::TILE_BYTES : 0) + row0 * (2 * D);
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
@@ -514,10 +530,10 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
     if (n + NST - 1 < ntiles) stage_tile(n + NST - 1);  // its stage held tile n - 1, done before the barrier
     int kh, j0;
     tile_pos(n, kh, j0);
-    const int kb0 = j0 / C, kb1 = (min(L, j0 + 32) - 1) / C;
+    const int kb0 = j0 / C, kb1 = (min(Lk, j0 + 32) - 1) / C;
     bool any = false, all = false;
     if (wave_live) classify(qh, qb0, qb1, kh, kb0, kb1, a.leak, any, all);
-    const bool ragged = (j0 + 32 > L) || (r1 - r0 < 32);
+    const bool ragged = (j0 + 32 > Lk) || (r1 - r0 < 32);
     const unsigned char* Ks = smem + (n % NST) * SM::STAGE;
     const unsigned char* Vs = Ks + SM::TILE_BYTES;
     if (any) {
@@ -534,11 +550,11 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
       for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;
       if (!all || ragged) {
         const int qi = r0 + l32;
-        const int qbl = qi / C;
+        const int qbl = (qa + qi) / C;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int kj = j0 + rho(v, h);
-          const bool okk = kj < L && qi < L && visible(qh, qbl, kh, kj / C, a.leak);
+          const bool okk = kj < Lk && qi < Lq && visible(qh, qbl, kh, kj / C, a.leak);
           st[v] = okk ? st[v] : -INFINITY;
         }
       }
@@ -591,9 +607,10 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   }
 
   const int qi = r0 + l32;
-  if (wave_live && qi < L) {
+  if (wave_live && qi < Lq) {
     const float inv = 1.f / lrow;
-    bf16* op = (bf16*)a.out + (((long long)b * 2 * L + qh * L + qi) * a.Hq + hq) * a.d + e * DH;
+    const long long orow = BC ? (long long)b * Lq + qi : (long long)b * 2 * L + qh * L + qi;
+    bf16* op = (bf16*)a.out + (orow * a.Hq + hq) * a.d + e * DH;
 #pragma unroll
     for (int t = 0; t < SH; ++t)
 #pragma unroll
@@ -606,19 +623,63 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   }
 }
 
-template <int D>
+template <int D, bool BC>
 static int launch_attn_dma(const AttnArgs& a, hipStream_t st) {
-  const int ntq = (a.L + 31) / 32;
+  const int ntq = ((BC ? a.M : a.L) + 31) / 32;
   const int ng = (ntq + 3) / 4;
-  const long long nblk = (long long)ng * 2 * a.B * a.Hq;
+  const long long nblk = (long long)ng * (BC ? 1 : 2) * a.B * a.Hq;
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "attention: grid too large");
-  bd_attn_dma_kernel<D><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  bd_attn_dma_kernel<D, BC><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention launch: %s", hipGetErrorString(e));
   return DLLM_OK;
 }
 
 static bool fits32(long long x) { return x >= -2147483647LL && x <= 2147483647LL; }
+
+// shared by both entry points: vectorisation check and kernel choice
+template <bool BC>
+static int dispatch_attn(AttnArgs& a, const int64_t* const sts[3], int dtype, hipStream_t st) {
+  const int d = a.d;
+  const int esz = dtype == DT_BF16 ? 2 : 4;
+  const int vel = 16 / esz;
+  const int dw = d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : 256;
+  bool vec = (d == dw);
+  for (int i = 0; i < 3; ++i) vec = vec && (sts[i][0] % vel == 0) && (sts[i][1] % vel == 0) && (sts[i][2] % vel == 0);
+  vec = vec && ((uintptr_t)a.q % 16 == 0) && ((uintptr_t)a.k % 16 == 0) && ((uintptr_t)a.v % 16 == 0);
+  a.vec = vec;
+  if (dtype == DT_BF16) {
+    // the direct-load kernel needs whole 16-byte rows of exactly d elements (vectorisable layout)
+    if (vec && d == dw && dw >= 64 && (a.k_st % 8) == 0 && (a.v_st % 8) == 0) {
+      switch (dw) {
+        case 64: return launch_attn_dma<64, BC>(a, st);
+        case 128: return launch_attn_dma<128, BC>(a, st);
+        default: return launch_attn_dma<256, BC>(a, st);
+      }
+    }
+    switch (dw) {
+      case 32: return launch_attn<32, true, BC>(a, st);
+      case 64: return launch_attn<64, true, BC>(a, st);
+      case 128: return launch_attn<128, true, BC>(a, st);
+      default: return launch_attn<256, true, BC>(a, st);
+    }
+  }
+  if (dtype == DT_F32) {
+    switch (dw) {
+      case 32: return launch_attn<32, false, BC>(a, st);
+      case 64: return launch_attn<64, false, BC>(a, st);
+      case 128: return launch_attn<128, false, BC>(a, st);
+      default: return launch_attn<256, false, BC>(a, st);
+    }
+  }
+  return fail(DLLM_EUNSUPPORTED, "attention: dtype %d not supported", dtype);
+}
+
+static void fill_strides(AttnArgs& a, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides) {
+  a.q_sb = q_strides[0]; a.q_st = (int)q_strides[1]; a.q_sh = (int)q_strides[2];
+  a.k_sb = k_strides[0]; a.k_st = (int)k_strides[1]; a.k_sh = (int)k_strides[2];
+  a.v_sb = v_strides[0]; a.v_st = (int)v_strides[1]; a.v_sh = (int)v_strides[2];
+}
 
 }  // namespace dllm
 
@@ -634,7 +695,7 @@ extern "C" int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, co
   if (L % block) return fail(DLLM_EINVAL, "L=%d is not a multiple of block=%d", L, block);
   if (Hq % Hkv) return fail(DLLM_EINVAL, "attention: Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
   if (d > 256) return fail(DLLM_EUNSUPPORTED, "attention: head_dim %d > 256 not supported", d);
-  const int64_t* sts[3] = {q_strides, k_strides, v_strides};
+  const int64_t* const sts[3] = {q_strides, k_strides, v_strides};
   const int H[3] = {Hq, Hkv, Hkv};
   for (int i = 0; i < 3; ++i)
     if (!fits32(2LL * L * sts[i][1]) || !fits32((long long)H[i] * sts[i][2]) ||
@@ -642,43 +703,37 @@ extern "C" int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, co
       return fail(DLLM_EUNSUPPORTED, "attention: per-sequence extent exceeds 32-bit element offsets");
   AttnArgs a = {};
   a.q = q; a.k = k; a.v = v; a.out = out;
-  a.q_sb = q_strides[0]; a.q_st = (int)q_strides[1]; a.q_sh = (int)q_strides[2];
-  a.k_sb = k_strides[0]; a.k_st = (int)k_strides[1]; a.k_sh = (int)k_strides[2];
-  a.v_sb = v_strides[0]; a.v_st = (int)v_strides[1]; a.v_sh = (int)v_strides[2];
+  fill_strides(a, q_strides, k_strides, v_strides);
   a.B = B; a.L = L; a.Hq = Hq; a.Hkv = Hkv; a.d = d; a.C = block;
   a.leak = flags & 1;
   a.scale_log2e = scale * 1.4426950408889634f;
-  const int esz = dtype == DT_BF16 ? 2 : 4;
-  const int vel = 16 / esz;
-  const int dw = d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : 256;
-  bool vec = (d == dw);
-  for (int i = 0; i < 3; ++i) vec = vec && (sts[i][0] % vel == 0) && (sts[i][1] % vel == 0) && (sts[i][2] % vel == 0);
-  vec = vec && ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0);
-  a.vec = vec;
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == DT_BF16) {
-    // the direct-load kernel needs whole 16-byte rows of exactly d elements (vectorisable layout)
-    if (vec && d == dw && dw >= 64 && (a.k_st % 8) == 0 && (a.v_st % 8) == 0) {
-      switch (dw) {
-        case 64: return launch_attn_dma<64>(a, st);
-        case 128: return launch_attn_dma<128>(a, st);
-        default: return launch_attn_dma<256>(a, st);
-      }
-    }
-    switch (dw) {
-      case 32: return launch_attn<32, true>(a, st);
-      case 64: return launch_attn<64, true>(a, st);
-      case 128: return launch_attn<128, true>(a, st);
-      default: return launch_attn<256, true>(a, st);
-    }
-  }
-  if (dtype == DT_F32) {
-    switch (dw) {
-      case 32: return launch_attn<32, false>(a, st);
-      case 64: return launch_attn<64, false>(a, st);
-      case 128: return launch_attn<128, false>(a, st);
-      default: return launch_attn<256, false>(a, st);
-    }
-  }
-  return fail(DLLM_EUNSUPPORTED, "attention: dtype %d not supported", dtype);
+  return dispatch_attn<false>(a, sts, dtype, (hipStream_t)stream);
+}
+
+extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, const void* k,
+                                               const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                               void* out, int B, int M, int N, int q0, int Hq, int Hkv, int d,
+                                               int block, float scale, int dtype, void* stream) {
+  if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides)
+    return fail(DLLM_EINVAL, "block-causal attention: null pointer");
+  if (B <= 0 || M <= 0 || N <= 0 || q0 < 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || block <= 0)
+    return fail(DLLM_EINVAL, "block-causal attention: bad sizes B=%d M=%d N=%d q0=%d Hq=%d Hkv=%d d=%d block=%d", B,
+                M, N, q0, Hq, Hkv, d, block);
+  if ((long long)q0 + M > 0x7fffffffLL) return fail(DLLM_EINVAL, "block-causal attention: q0 + M overflows");
+  if (Hq % Hkv) return fail(DLLM_EINVAL, "attention: Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+  if (d > 256) return fail(DLLM_EUNSUPPORTED, "attention: head_dim %d > 256 not supported", d);
+  const int64_t* const sts[3] = {q_strides, k_strides, v_strides};
+  const int H[3] = {Hq, Hkv, Hkv};
+  const int rows[3] = {M, N, N};
+  for (int i = 0; i < 3; ++i)
+    if (!fits32((long long)rows[i] * sts[i][1]) || !fits32((long long)H[i] * sts[i][2]) ||
+        !fits32((long long)rows[i] * sts[i][1] + (long long)H[i] * sts[i][2]))
+      return fail(DLLM_EUNSUPPORTED, "attention: per-sequence extent exceeds 32-bit element offsets");
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.out = out;
+  fill_strides(a, q_strides, k_strides, v_strides);
+  a.B = B; a.L = 0; a.Hq = Hq; a.Hkv = Hkv; a.d = d; a.C = block;
+  a.M = M; a.N = N; a.q0 = q0;
+  a.scale_log2e = scale * 1.4426950408889634f;
+  return dispatch_attn<true>(a, sts, dtype, (hipStream_t)stream);
 }

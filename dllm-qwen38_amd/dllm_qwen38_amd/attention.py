@@ -74,6 +74,41 @@ def bd_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: in
     return out
 
 
+def block_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int, q_offset: int = 0,
+                           scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Block-causal attention of a query segment against a key/value cache (the clean-prefix cache
+    of the cached decoder; the reference re-runs the whole forward instead, decode.py:63-66).
+
+    q [B, M, Hq, d] at absolute positions q_offset..q_offset+M-1; k/v [B, N, Hkv, d] at positions
+    0..N-1 (token-major, any batch/token/head strides, last dim contiguous; rotary already applied).
+    Query i sees key j iff j // block <= (q_offset + i) // block (blockdiff.py:43-47 with the query
+    rows offset). Returns [B, M, Hq, d]."""
+    dev = _lib.require_device(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q must be [B, M, Hq, d] and k, v [B, N, Hkv, d]")
+    B, M, Hq, d = q.shape
+    N, Hkv = k.shape[1], k.shape[2]
+    if k.shape[0] != B or v.shape != k.shape or k.shape[-1] != d:
+        raise ValueError("k and v must be [B, N, Hkv, d] matching q")
+    if Hq % Hkv:
+        raise ValueError(f"query heads {Hq} not a multiple of key/value heads {Hkv}")
+    if q_offset < 0 or block <= 0:
+        raise ValueError(f"q_offset {q_offset} and block {block} must be >= 0 and > 0")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k, v dtypes differ")
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    if out is None:
+        out = torch.empty(B, M, Hq, d, dtype=q.dtype, device=dev)
+    elif tuple(out.shape) != (B, M, Hq, d) or not out.is_contiguous() or out.dtype != q.dtype:
+        raise ValueError("out must be a contiguous [B, M, Hq, d] tensor of q's dtype")
+    sc = d ** -0.5 if scale is None else float(scale)
+    _lib.check(_lib.lib().dllm_block_causal_attention_fwd(
+        q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
+        out.data_ptr(), B, M, N, q_offset, Hq, Hkv, d, block, sc, _lib.dtype_code(q.dtype), _lib.stream_handle(dev)),
+        "dllm_block_causal_attention_fwd")
+    return out
+
+
 def attention_flops(B: int, L: int, Hq: int, d: int, block: int, leak: bool = False) -> int:
     """Algorithmic flops over the visible (query, key) pairs only: 4*d per pair and query head."""
     nb = L // block

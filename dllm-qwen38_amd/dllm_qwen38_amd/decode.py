@@ -1,0 +1,288 @@
+"""Block-wise confidence-threshold parallel decoding on the MI355X HIP kernels.
+
+Drop-in for the reference's `src/dllm_qwen38/decode.py`:
+  * `DecodeTrace` and `generate` (decode.py:23-99): the golden decoder. Every denoising step re-runs
+    the whole two-stream `block_diffusion_forward` over prompt + generated tokens, here on the HIP
+    path, so its temperature-0 token stream is the one a faster decoder must reproduce.
+  * `generate_cached`: the same decoder with the clean prefix kept on the device instead of
+    recomputed. Under the complementary mask, x_t block k sees x_0 blocks < k and itself, and x_0
+    is block-causal; so the noised logits of block k are a block-causal forward of the block's own
+    tokens on top of the clean prefix, whose per-layer state is everything the block needs:
+      - Gated DeltaNet layers: the recurrent state after the prefix [B, Hv, Dk, Dv] (fp32) and the
+        pre-conv projections of the prefix's last (conv width - 1) tokens (the conv carry-in);
+      - attention layers: the prefix's keys and values after q/k norm and RoPE.
+    A denoising step is then one forward over `block` tokens instead of (k + 1) * block, and a
+    finished block enters the cache with one more such forward (`commit`). The prompt's whole blocks
+    are prefilled in one block-causal forward.
+    `PrefixCache` holds that state in HBM and `forward_segment` runs a segment through it.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import attention, gdn, norms
+from .blockdiff import FULL, LINEAR, _eps, block_diffusion_forward, mlp, rmsnorm, rotary_tables
+
+
+@dataclass
+class DecodeTrace:
+    """Token stream and schedule of one decode (decode.py:23-33). `commits`: cache-extending
+    forwards of `generate_cached` (one per finished block, plus the prompt prefill); not counted in
+    `forwards`, which counts denoising forwards as the reference does."""
+
+    tokens: list[int]
+    forwards: int = 0
+    generated: int = 0
+    steps_per_block: list[int] = field(default_factory=list)
+    commits: int = 0
+
+    @property
+    def tokens_per_forward(self) -> float:
+        return self.generated / self.forwards if self.forwards else 0.0
+
+
+def _select(logits: torch.Tensor, masked: torch.Tensor, *, threshold: float, sub_block: int | None,
+            temperature: float):
+    """The commit rule of one denoising step (decode.py:67-88). logits [C, V] fp32 over the current
+    block, masked [C] bool. Returns (commit [C] bool, pick [C] tokens): the argmax token (a sample
+    at temperature > 0) and its probability per position; candidates are the masked positions,
+    restricted with sub_block to the leftmost sub-block still holding a mask; every candidate at or
+    above the threshold commits, and at least the most confident one does."""
+    if temperature > 0:
+        probs = torch.softmax(logits / temperature, -1)
+        pick = torch.multinomial(probs, 1).squeeze(1)
+        conf = probs.gather(1, pick.unsqueeze(1)).squeeze(1)
+    else:
+        conf, pick = torch.softmax(logits, -1).max(-1)
+    cand = masked.clone()
+    if sub_block:
+        first = int(masked.nonzero()[0])
+        start = (first // sub_block) * sub_block
+        cand[:start] = False
+        cand[start + sub_block:] = False
+    conf = conf.masked_fill(~cand, -1.0)
+    commit = cand & (conf >= threshold)
+    if not bool(commit.any()):
+        commit[int(conf.argmax())] = True
+    return commit, pick
+
+
+@torch.no_grad()
+def generate(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int, block: int, mask_id: int,
+             threshold: float = 0.9, sub_block: int | None = None, eos_id: int | None = None,
+             temperature: float = 0.0, layers: int | None = None) -> DecodeTrace:
+    """The golden decoder (decode.py:36-99): per block, start from all-mask, re-run the whole
+    two-stream forward per step and commit by `_select` until the block is clean; stop after the
+    block that produced `eos_id`."""
+    device = text_model.embed_tokens.weight.device
+    cur = list(prompt_ids)
+    trace = DecodeTrace(tokens=cur)
+    for _ in range(n_blocks):
+        n = len(cur)
+        kb = n // block
+        L = (kb + 1) * block
+        known = torch.full((L,), mask_id, dtype=torch.long, device=device)
+        known[:n] = torch.tensor(cur, dtype=torch.long, device=device)
+        masked = torch.arange(L, device=device) >= n
+        x0 = known.clone()  # x_0 block kb is invisible to x_t block kb
+        steps = 0
+        while bool(masked.any()):
+            xt = known.masked_fill(masked, mask_id)
+            lt, _ = block_diffusion_forward(text_model, lm_head, x0[None], xt[None], block, layers=layers)
+            trace.forwards += 1
+            steps += 1
+            commit, pick = _select(lt[0, kb * block:].float(), masked[kb * block:], threshold=threshold,
+                                   sub_block=sub_block, temperature=temperature)
+            known[kb * block:][commit] = pick[commit]
+            masked[kb * block:][commit] = False
+        trace.steps_per_block.append(steps)
+        new = known[n:].tolist()
+        cur.extend(new)
+        trace.generated += len(new)
+        if eos_id is not None and eos_id in new:
+            break
+    trace.tokens = cur
+    return trace
+
+
+class PrefixCache:
+    """Per-layer state of a committed clean prefix, resident in HBM, for `forward_segment`.
+
+    For each Gated DeltaNet layer: `state[i]` [B, Hv, Dk, Dv] fp32 (the recurrence after the prefix)
+    and `conv[i]` [B, conv_dim, width - 1] (pre-conv projections of the prefix's last tokens), both
+    None while the prefix is empty. For each attention layer: `k[i]`, `v[i]` [B, capacity, Hkv, d]
+    (after q/k norm and RoPE); rows >= `length` are scratch. `length` is the committed prefix in
+    tokens, a multiple of `block`."""
+
+    def __init__(self, text_model, *, batch: int, capacity: int, block: int, layers: int | None = None):
+        cfg = text_model.config
+        self.n_layers = cfg.num_hidden_layers if layers is None else layers
+        if not 0 < self.n_layers <= cfg.num_hidden_layers:
+            raise ValueError(f"layers={layers} outside 1..{cfg.num_hidden_layers}")
+        if block <= 0 or capacity <= 0 or capacity % block:
+            raise ValueError(f"capacity {capacity} must be a positive multiple of block {block}")
+        w = text_model.embed_tokens.weight
+        self.device, self.dtype = w.device, w.dtype
+        self.batch, self.capacity, self.block, self.length = batch, capacity, block, 0
+        self.kinds = list(cfg.layer_types[: self.n_layers])
+        self.state: dict[int, torch.Tensor | None] = {}
+        self.conv: dict[int, torch.Tensor | None] = {}
+        self.k: dict[int, torch.Tensor] = {}
+        self.v: dict[int, torch.Tensor] = {}
+        for i, kind in enumerate(self.kinds):
+            if kind == LINEAR:
+                self.state[i] = self.conv[i] = None
+            elif kind == FULL:
+                att = text_model.layers[i].self_attn
+                hkv = att.k_proj.out_features // att.head_dim
+                shape = (batch, capacity, hkv, att.head_dim)
+                self.k[i] = torch.empty(shape, dtype=self.dtype, device=self.device)
+                self.v[i] = torch.empty(shape, dtype=self.dtype, device=self.device)
+            else:
+                raise ValueError(f"unknown layer type {kind}")
+        self.cos, self.sin = rotary_tables(text_model, capacity, self.device, self.dtype)
+
+    def reset(self) -> None:
+        """Forget the prefix (buffers are kept)."""
+        self.length = 0
+        for i in self.state:
+            self.state[i] = self.conv[i] = None
+
+    def nbytes(self) -> int:
+        tens = [t for d in (self.state, self.conv, self.k, self.v) for t in d.values() if t is not None]
+        return sum(t.numel() * t.element_size() for t in tens)
+
+
+def _gdn_segment(m, x: torch.Tensor, cache: PrefixCache, i: int, commit: bool) -> torch.Tensor:
+    """Gated DeltaNet mixer of a segment on top of the cached prefix (the reference's
+    gdn_mixer_forward with conv_prefix / initial_state, gdn.py:193-233): the conv carries the
+    prefix's last projections in, the recurrence starts from the prefix state; with commit, the
+    state after the segment and its last projections replace the cached ones."""
+    B, T, _ = x.shape
+    raw = m.in_proj_qkv(x)  # [B, T, conv_dim]
+    z = m.in_proj_z(x)
+    beta, g = gdn._beta_g(m, m.in_proj_b(x), m.in_proj_a(x))
+    mixed = gdn.causal_conv1d_fn(raw.transpose(1, 2), m.conv1d.weight.squeeze(1), m.conv1d.bias,
+                                 activation=m.activation, conv_prefix=cache.conv[i]).transpose(1, 2)
+    q, k, v = gdn._split_qkv(mixed, m, B, T)
+    core, states = gdn._core(q, k, v, g, beta, chunk_size=cache.block, initial_state=cache.state[i],
+                             need_states=commit)
+    if commit:
+        km1 = m.conv1d.weight.shape[-1] - 1
+        hist = raw.transpose(1, 2) if cache.conv[i] is None or T >= km1 else torch.cat([cache.conv[i], raw.transpose(1, 2)], 2)
+        if hist.shape[2] < km1:  # a prefix shorter than the conv window: zero history before it
+            hist = torch.nn.functional.pad(hist, (km1 - hist.shape[2], 0))
+        cache.conv[i] = hist[:, :, -km1:].contiguous()
+        cache.state[i] = states[:, -1].contiguous()
+    Dv = m.head_v_dim
+    o = norms.gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm.weight, _eps(m.norm))
+    return m.out_proj(o.reshape(B, T, -1))
+
+
+def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: int) -> torch.Tensor:
+    """Gated attention of a segment at positions pos0.. over the cached prefix ([hf]:656-701 under
+    the block-causal rule): q/k norm + RoPE, the segment's K/V written into the cache at pos0..,
+    block-causal attention against cache rows 0..pos0+T-1, sigmoid gate, o_proj."""
+    B, T, _ = x.shape
+    hd = att.head_dim
+    q, gate = torch.chunk(att.q_proj(x).view(B, T, -1, 2 * hd), 2, dim=-1)
+    gate = gate.reshape(B, T, -1)
+    cos, sin = cache.cos[pos0:pos0 + T], cache.sin[pos0:pos0 + T]
+    q, k = norms.qk_norm_rope(q, att.k_proj(x).view(B, T, -1, hd), att.q_norm, att.k_norm, cos, sin, T)
+    cache.k[i][:, pos0:pos0 + T] = k
+    cache.v[i][:, pos0:pos0 + T] = att.v_proj(x).view(B, T, -1, hd)
+    o = attention.block_causal_attention(q, cache.k[i][:, :pos0 + T], cache.v[i][:, :pos0 + T], block=cache.block,
+                                         q_offset=pos0, scale=float(att.scaling))
+    return att.o_proj(o.reshape(B, T, -1) * torch.sigmoid(gate))
+
+
+@torch.no_grad()
+def forward_segment(text_model, lm_head, cache: PrefixCache, ids: torch.Tensor, *, commit: bool,
+                    logits: bool = True):
+    """Run ids [B, T] (T a multiple of the block) at positions cache.length.. through the stack on
+    top of the cached prefix, block-causally. Returns the logits [B, T, V] (or None with
+    logits=False). With commit, the segment becomes part of the prefix; without, the cache's
+    committed state is untouched (attention rows past `length` are scratch). Runs without autograd:
+    the HIP kernels are forward-only."""
+    if ids.dim() != 2 or ids.shape[0] != cache.batch:
+        raise ValueError(f"ids must be [B={cache.batch}, T]")
+    B, T = ids.shape
+    P = cache.length
+    if T == 0 or T % cache.block:
+        raise ValueError(f"segment length {T} is not a positive multiple of block={cache.block}")
+    if P + T > cache.capacity:
+        raise ValueError(f"segment at {P}..{P + T} exceeds the cache capacity {cache.capacity}")
+    h = text_model.embed_tokens(ids)
+    pending = None
+    for i, kind in enumerate(cache.kinds):
+        layer = text_model.layers[i]
+        if pending is None:
+            x = rmsnorm(h, layer.input_layernorm)
+        else:
+            x, h = rmsnorm(pending, layer.input_layernorm, residual=h)
+        if kind == LINEAR:
+            o = _gdn_segment(layer.linear_attn, x, cache, i, commit)
+        else:
+            o = _attention_segment(layer.self_attn, x, cache, i, P)
+        x, h = rmsnorm(o, layer.post_attention_layernorm, residual=h)
+        pending = mlp(layer.mlp, x)
+    if commit:
+        cache.length = P + T
+    if not logits:
+        return None
+    return lm_head(rmsnorm(pending, text_model.norm, residual=h)[0])
+
+
+@torch.no_grad()
+def generate_cached(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int, block: int, mask_id: int,
+                    threshold: float = 0.9, sub_block: int | None = None, eos_id: int | None = None,
+                    temperature: float = 0.0, layers: int | None = None,
+                    cache: PrefixCache | None = None) -> DecodeTrace:
+    """`generate` with the clean prefix cached: same arguments, same commit rule and trace, one
+    block per denoising forward. The prompt's whole blocks are prefilled in one forward; each
+    finished block is committed with one more. A `cache` of batch 1 and enough capacity may be
+    passed in to reuse its buffers (it is reset)."""
+    device = text_model.embed_tokens.weight.device
+    cur = list(prompt_ids)
+    trace = DecodeTrace(tokens=cur)
+    kb = len(cur) // block
+    need = (kb + n_blocks) * block
+    if cache is None:
+        cache = PrefixCache(text_model, batch=1, capacity=need, block=block, layers=layers)
+    elif cache.batch != 1 or cache.capacity < need or cache.block != block:
+        raise ValueError("cache must have batch 1, the same block and capacity >= (prompt blocks + n_blocks) * block")
+    cache.reset()
+    if kb:
+        forward_segment(text_model, lm_head, cache, torch.tensor([cur[:kb * block]], device=device), commit=True,
+                        logits=False)
+        trace.commits += 1
+    for nb in range(n_blocks):
+        n = len(cur)
+        kb = n // block
+        have = n - kb * block  # prompt tokens already in this block
+        known = torch.full((block,), mask_id, dtype=torch.long, device=device)
+        known[:have] = torch.tensor(cur[kb * block:], dtype=torch.long, device=device)
+        masked = torch.arange(block, device=device) >= have
+        steps = 0
+        while bool(masked.any()):
+            lt = forward_segment(text_model, lm_head, cache, known.masked_fill(masked, mask_id)[None], commit=False)
+            trace.forwards += 1
+            steps += 1
+            commit, pick = _select(lt[0].float(), masked, threshold=threshold, sub_block=sub_block,
+                                   temperature=temperature)
+            known[commit] = pick[commit]
+            masked[commit] = False
+        trace.steps_per_block.append(steps)
+        new = known[have:].tolist()
+        cur.extend(new)
+        trace.generated += len(new)
+        done = eos_id is not None and eos_id in new
+        if done or nb == n_blocks - 1:
+            break
+        forward_segment(text_model, lm_head, cache, known[None], commit=True, logits=False)
+        trace.commits += 1
+    trace.tokens = cur
+    return trace

@@ -124,6 +124,21 @@ int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, const void* k
                           int d, int block, float scale, int dtype, int flags, void* stream);
 
 /*
+ * Block-causal attention of a query segment against a key/value cache: the clean-prefix cache of a
+ * cached decoder. The reference decoder (src/dllm_qwen38/decode.py:63-66) re-runs the whole
+ * two-stream forward per denoising step; there, x_t block k sees x_0 blocks < k and itself
+ * (blockdiff.py:50-66), and the clean stream is block-causal (blockdiff.py:43-47). With the clean
+ * prefix's K/V kept, one step is this call with the block's queries. q [B,M,Hq,d] at absolute
+ * positions q0..q0+M-1; k/v [B,N,Hkv,d] at positions 0..N-1 (rotary already applied); query i sees
+ * key j iff j/block <= (q0+i)/block. A denoising step is M = block, q0 = N - block (every key
+ * visible); a prompt prefill is q0 = 0, M = N. Strides {b,t,h} in elements, last dim contiguous;
+ * out [B,M,Hq,d] contiguous, same dtype. Same numerics as dllm_bd_attention_fwd; d <= 256.
+ */
+int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                    const void* v, const int64_t* v_strides, void* out, int B, int M, int N, int q0,
+                                    int Hq, int Hkv, int d, int block, float scale, int dtype, void* stream);
+
+/*
  * Qwen3.5 RMSNorm over the last dim of x [rows, dim]: y = x * rsqrt(mean(x^2) + eps) * (1 + w)
  * in fp32 (unit_offset = 1; 0 applies w as is), rounded once to x's dtype.
  * Replaces [hf]:720-737 Qwen3_5RMSNorm as called by the decoder layer and the final norm

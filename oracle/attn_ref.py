@@ -15,6 +15,9 @@ How each function is pinned (tests/test_oracle_attn.py):
   bd_attention     float64 brute force: dense softmax over the materialised mask, repeat_kv'd
                    keys; RoPE checked against transformers' own apply_rotary_pos_emb and rotary
                    module on a tiny config.
+  block_causal_attention
+                   the x_0 half of the float64 brute force (the clean stream is block-causal), at
+                   every query offset (a segment at offset q0 equals rows q0.. of the prefill).
 """
 
 from __future__ import annotations
@@ -109,6 +112,25 @@ def bd_attention(q, k, v, *, block: int, rotary_dim: int = 0, rope_base: float =
         sc = sc.masked_fill(~allowed[s0:s1], float("-inf"))
         out[:, :, s0:s1] = torch.softmax(sc, -1) @ vx
     return out.permute(0, 2, 1, 3).contiguous()
+
+
+def block_causal_attention(q, k, v, *, block: int, q_offset: int = 0, scale: float | None = None):
+    """Block-causal GQA attention of a query segment against a key cache, float32 on the CPU: the
+    x_0 -> x_0 rule of the complementary mask (blockdiff.py:43-47, 61-62) with the queries at
+    absolute positions q_offset.. and the keys at 0..N-1. q [B,M,Hq,d], k/v [B,N,Hkv,d], rotary
+    already applied. Returns [B,M,Hq,d] float32. This is what one step of a decoder that keeps the
+    clean prefix's K/V computes instead of re-running the forward (decode.py:63-66)."""
+    B, M, Hq, d = q.shape
+    N, Hkv = k.shape[1], k.shape[2]
+    scale = d ** -0.5 if scale is None else scale
+    qb = (torch.arange(M) + q_offset) // block
+    kb = torch.arange(N) // block
+    allowed = kb[None, :] <= qb[:, None]
+    kx = k.float().repeat_interleave(Hq // Hkv, dim=2).permute(0, 2, 1, 3)
+    vx = v.float().repeat_interleave(Hq // Hkv, dim=2).permute(0, 2, 1, 3)
+    sc = (q.float().permute(0, 2, 1, 3) @ kx.transpose(-1, -2)) * scale
+    sc = sc.masked_fill(~allowed, float("-inf"))
+    return (torch.softmax(sc, -1) @ vx).permute(0, 2, 1, 3).contiguous()
 
 
 def bd_attention_f64_bruteforce(q, k, v, *, block: int, rotary_dim: int = 0, rope_base: float = 1e7,

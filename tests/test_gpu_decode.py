@@ -1,0 +1,179 @@
+"""GPU parity of the cached decoder and its block-causal attention kernel.
+
+Bars:
+  * block-causal attention vs the CPU oracle: fp32 <= 1e-5 max-abs; bf16 within
+    2^-8 * max|V| + 2^-7 * |ref| (P rounded to bf16 before P.V, output rounded to bf16), the bar
+    of the complementary-mask kernel; and bit-equal to the clean half of that kernel, whose rows
+    walk the same key tiles in the same order;
+  * fp32 tiny model: the logits of a cached denoising step vs the per-block oracle and vs the
+    two-stream forward <= 1e-4 max-abs (the fork forward's own bar);
+  * token streams at temperature 0: `generate` (golden, HIP forward) and `generate_cached` equal the
+    oracle decoder's on the tiny fp32 model;
+  * 27B-class geometry in bf16: a cached step's logits vs the two-stream forward's within
+    2^-5 * max|logits| + 2^-6 * |logit| (bf16 activations, different GEMM shapes on each side).
+"""
+
+import copy
+
+import pytest
+import torch
+
+from _tiny import tiny_hf_model
+from dllm_qwen38_amd import attention, blockdiff, decode
+from dllm_qwen38_amd import model as hybrid
+from oracle import attn_ref, decode_ref, model_ref
+
+pytestmark = pytest.mark.gpu
+
+F32_ATT = 1e-5
+F32_LOGITS = 1e-4
+
+
+def _att_inputs(B, M, N, Hq, Hkv, d, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, M, Hq, d, generator=g).to(dtype)
+    k = torch.randn(B, N, Hkv, d, generator=g).to(dtype)
+    v = torch.randn(B, N, Hkv, d, generator=g).to(dtype)
+    return q, k, v
+
+
+def _check_att(got, ref, dtype, vmax, name):
+    err = (got.float().cpu() - ref.float()).abs()
+    print(f"{name}: max|d|={err.max().item():.3e}")
+    if dtype == torch.float32:
+        assert err.max().item() <= F32_ATT, name
+    else:
+        assert (err <= 2 ** -8 * vmax + 2 ** -7 * ref.float().abs()).all(), name
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,M,N,q0,Hq,Hkv,d,block", [
+    (1, 32, 1024, 992, 6, 2, 256, 32),   # a decoding step: every key visible
+    (2, 160, 160, 0, 4, 2, 128, 32),     # a prompt prefill: block-causal from 0
+    (1, 16, 112, 96, 4, 4, 64, 16),      # decoding step, block 16
+    (2, 20, 100, 80, 4, 2, 64, 20),      # ragged: N, M not multiples of 32
+    (1, 37, 70, 33, 4, 2, 16, 8),        # the tiny model's head size; q0 inside a block
+    (1, 64, 96, 32, 2, 1, 80, 32),       # d outside the direct-load kernel's set
+])
+def test_block_causal_attention_matches_oracle(dev, dtype, B, M, N, q0, Hq, Hkv, d, block):
+    q, k, v = _att_inputs(B, M, N, Hq, Hkv, d, dtype, seed=M + N + d)
+    got = attention.block_causal_attention(q.to(dev), k.to(dev), v.to(dev), block=block, q_offset=q0)
+    torch.cuda.synchronize()
+    ref = attn_ref.block_causal_attention(q, k, v, block=block, q_offset=q0)
+    _check_att(got, ref, dtype, v.float().abs().max().item(), f"{dtype} M{M} N{N} q0{q0} d{d} block{block}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L,d,block", [(256, 256, 32), (96, 64, 16), (40, 16, 8)])
+def test_prefill_is_bit_equal_to_the_clean_half_of_the_two_stream_kernel(dev, dtype, L, d, block):
+    g = torch.Generator().manual_seed(L + d)
+    q, k, v = (torch.randn(2, 2 * L, h, d, generator=g).to(dtype).to(dev) for h in (4, 2, 2))
+    both = attention.bd_attention(q, k, v, block=block)
+    clean = attention.block_causal_attention(q[:, L:], k[:, L:], v[:, L:], block=block)
+    torch.cuda.synchronize()
+    assert torch.equal(clean, both[:, L:])
+
+
+def test_27b_class_decoding_step_attention(dev):
+    """24 query / 4 key-value heads of dim 256, 4096 cached keys, one block of 32 queries."""
+    q, k, v = _att_inputs(1, 32, 4096, 24, 4, 256, torch.bfloat16, seed=27)
+    got = attention.block_causal_attention(q.to(dev), k.to(dev), v.to(dev), block=32, q_offset=4064)
+    torch.cuda.synchronize()
+    ref = attn_ref.block_causal_attention(q, k, v, block=32, q_offset=4064)
+    _check_att(got, ref, torch.bfloat16, v.float().abs().max().item(), "27b step")
+
+
+@pytest.fixture(scope="module")
+def tiny(dev):
+    cpu_model, cpu_head = tiny_hf_model(seed=0)
+    return cpu_model, cpu_head, copy.deepcopy(cpu_model).to(dev), copy.deepcopy(cpu_head).to(dev)
+
+
+def _maxdiff(a, b):
+    return (a.float().cpu() - b.float().cpu()).abs().max().item()
+
+
+@pytest.mark.parametrize("block,prompt_blocks", [(8, 3), (16, 2), (4, 5)])
+def test_cached_step_matches_the_per_block_oracle_and_the_forward(tiny, dev, block, prompt_blocks):
+    cm, ch, gm, gh = tiny
+    g = torch.Generator().manual_seed(block)
+    P = prompt_blocks * block
+    x0 = torch.randint(0, 255, (1, P + block), generator=g)
+    xt = x0.clone()
+    xt[:, P:][torch.rand(1, block, generator=g) < 0.5] = 255
+    cache = decode.PrefixCache(gm, batch=1, capacity=P + 2 * block, block=block)
+    decode.forward_segment(gm, gh, cache, x0[:, :P].to(dev), commit=True, logits=False)
+    step = decode.forward_segment(gm, gh, cache, xt[:, P:].to(dev), commit=False)
+    again = decode.forward_segment(gm, gh, cache, xt[:, P:].to(dev), commit=False)
+    with torch.no_grad():
+        lt, _ = blockdiff.block_diffusion_forward(gm, gh, x0.to(dev), xt.to(dev), block)
+    torch.cuda.synchronize()
+    assert cache.length == P
+    assert torch.equal(step, again)  # an uncommitted step leaves the prefix untouched
+    ref = model_ref.reference_block_logits(cm, ch, x0, xt, block)[:, P:]
+    d_ref, d_fwd = _maxdiff(step, ref), _maxdiff(step, lt[:, P:])
+    print(f"block {block} prefix {P}: vs per-block oracle {d_ref:.2e}, vs two-stream forward {d_fwd:.2e}")
+    assert d_ref <= F32_LOGITS and d_fwd <= F32_LOGITS
+
+
+def test_block_by_block_commits_equal_one_prefill(tiny, dev):
+    _, _, gm, gh = tiny
+    block = 8
+    ids = torch.randint(0, 255, (1, 5 * block), generator=torch.Generator().manual_seed(3)).to(dev)
+    a = decode.PrefixCache(gm, batch=1, capacity=6 * block, block=block)
+    b = decode.PrefixCache(gm, batch=1, capacity=6 * block, block=block)
+    decode.forward_segment(gm, gh, a, ids[:, : 4 * block], commit=True, logits=False)
+    for j in range(4):
+        decode.forward_segment(gm, gh, b, ids[:, j * block:(j + 1) * block], commit=True, logits=False)
+    la = decode.forward_segment(gm, gh, a, ids[:, 4 * block:], commit=False)
+    lb = decode.forward_segment(gm, gh, b, ids[:, 4 * block:], commit=False)
+    torch.cuda.synchronize()
+    assert a.length == b.length == 4 * block
+    d = _maxdiff(la, lb)
+    print(f"one prefill vs four commits: {d:.2e}")
+    assert d <= 1e-5
+
+
+@pytest.mark.parametrize("prompt,block,threshold,sub_block", [
+    ([10, 11, 12, 13, 14], 8, 0.9, None),   # the reference's seam-test setting
+    (list(range(30, 46)), 8, 0.0, None),     # prompt of whole blocks, everything at once
+    ([5, 6, 7], 8, 0.0, 4),                  # sub-blocks
+])
+def test_token_streams_match_the_oracle_decoder(tiny, dev, prompt, block, threshold, sub_block):
+    cm, ch, gm, gh = tiny
+    kw = dict(n_blocks=3, block=block, mask_id=255, threshold=threshold, sub_block=sub_block)
+    ref = decode_ref.generate(cm, ch, prompt, **kw)
+    gold = decode.generate(gm, gh, prompt, **kw)
+    fast = decode.generate_cached(gm, gh, prompt, **kw)
+    print(f"oracle {ref['tokens']}\ngolden {gold.tokens}\ncached {fast.tokens}")
+    assert gold.tokens == ref["tokens"] and gold.steps_per_block == ref["steps_per_block"]
+    assert fast.tokens == ref["tokens"] and fast.steps_per_block == ref["steps_per_block"]
+    assert gold.forwards == fast.forwards == ref["forwards"]
+    assert fast.commits == (1 if len(prompt) >= block else 0) + 2
+
+
+@pytest.fixture(scope="module")
+def stack27(dev):
+    c = hybrid.config_27b_truncated(layers=4)
+    return hybrid.build(c, device=dev, dtype=torch.bfloat16, seed=21)
+
+
+def test_27b_class_cached_step_matches_the_forward_bf16(stack27, dev):
+    model, lm_head = stack27
+    block, P = 32, 512
+    g = torch.Generator().manual_seed(8)
+    x0 = torch.randint(0, 151936, (1, P + block), generator=g).to(dev)
+    xt = x0.clone()
+    xt[:, P + 5:] = 151935
+    cache = decode.PrefixCache(model, batch=1, capacity=P + block, block=block)
+    decode.forward_segment(model, lm_head, cache, x0[:, :P], commit=True, logits=False)
+    step = decode.forward_segment(model, lm_head, cache, xt[:, P:], commit=False)
+    with torch.no_grad():
+        lt, _ = blockdiff.block_diffusion_forward(model, lm_head, x0, xt, block)
+    torch.cuda.synchronize()
+    ref = lt[:, P:].float()
+    err = (step.float() - ref).abs()
+    bound = 2 ** -5 * ref.abs().max() + 2 ** -6 * ref.abs()
+    print(f"27b-class bf16 step vs forward: max|d|={err.max().item():.3e} max|ref|={ref.abs().max().item():.3e}")
+    assert (err <= bound).all()
+    print(f"cache bytes {cache.nbytes()}")

@@ -63,6 +63,29 @@ def test_bd_attention_matches_float64_bruteforce(leak):
         assert np.abs(got.double().numpy() - ref).max() < 1e-5
 
 
+@pytest.mark.parametrize("block", [8, 5])
+def test_block_causal_attention_is_the_clean_half_of_the_bruteforce_at_every_offset(block):
+    """The x_0 rows of the complementary mask see x_0 block-causally and nothing of x_t, so the
+    clean half of the float64 brute force pins the prefill (q_offset 0); a query segment at offset
+    q0 must equal rows q0.. of it, with only the first q0 + M keys present (a decode step)."""
+    g = torch.Generator().manual_seed(5)
+    B, L, Hq, Hkv, d = 2, 30, 4, 2, 16
+    q = torch.randn(B, 2 * L, Hq, d, generator=g)
+    k = torch.randn(B, 2 * L, Hkv, d, generator=g)
+    v = torch.randn(B, 2 * L, Hkv, d, generator=g)
+    ref = attn_ref.bd_attention_f64_bruteforce(q, k, v, block=block)[:, L:]
+    qc, kc, vc = q[:, L:], k[:, L:], v[:, L:]
+    got = attn_ref.block_causal_attention(qc, kc, vc, block=block)
+    assert np.abs(got.double().numpy() - ref).max() < 1e-5
+    for q0, M in ((10, 10), (block, block), (3, 7), (L - block, block)):
+        n = min(L, (q0 + M + block - 1) // block * block)
+        seg = attn_ref.block_causal_attention(qc[:, q0:q0 + M], kc[:, :n], vc[:, :n], block=block, q_offset=q0)
+        assert np.abs(seg.double().numpy() - ref[:, q0:q0 + M]).max() < 1e-5
+    # a planted off-by-one in the query offset is caught
+    bad = attn_ref.block_causal_attention(qc[:, 9:19], kc, vc, block=block, q_offset=8)
+    assert np.abs(bad.double().numpy() - ref[:, 9:19]).max() > 1e-3
+
+
 def test_rope_matches_transformers_apply_rotary_and_rotary_module():
     from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
     from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding, apply_rotary_pos_emb

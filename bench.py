@@ -81,10 +81,11 @@ def main(argv=None):
     ap.add_argument("--calibration-copy-gib", type=float, default=0.0,
                     help="after the timed steps, copy this many GiB device-to-device (the reference transfer "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
-    ap.add_argument("--workload", default="gdn-layer", choices=["gdn-layer", "attention", "stack"],
+    ap.add_argument("--workload", default="gdn-layer", choices=["gdn-layer", "attention", "stack", "decode"],
                     help="gdn-layer (default, the headline metric); attention: the complementary-mask attention "
                          "layer kernel at B=2 L=4096 Hq=24 Hkv=4 d=256; stack: the 16-layer 27B-class "
-                         "two-stream forward at B=1 L=2048")
+                         "two-stream forward at B=1 L=2048; decode: one cached denoising step of that stack "
+                         "(a 32-token block over a 2048-token clean prefix)")
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the state-fork layer shards over (batch, value head) with no "
@@ -94,6 +95,8 @@ def main(argv=None):
         return bench_attention(a)
     if a.workload == "stack":
         return bench_stack(a)
+    if a.workload == "decode":
+        return bench_decode(a)
 
     import torch
 
@@ -308,6 +311,82 @@ def bench_stack(a):
                      "frac": tf / BF16_MFMA_PEAK_TFLOPS, "traffic": None},
         "algorithmic_tflop": fl / 1e12, "params": hybrid.param_count(model) + lm_head.weight.numel(),
         "wall_s_timed": wall, "cpu_baseline": None,
+    }
+    print(json.dumps(res))
+    return 0
+
+
+def bench_decode(a):
+    """One denoising step of the prefix-cached decoder on the 16-layer 27B-class stack: a 32-token
+    noised block at positions 2048..2079 over a committed 2048-token clean prefix, B=1, bf16, logits
+    of the block. At B=1 the step reads every weight once for 32 token rows, so it is bound by HBM:
+    the roofline's algorithmic bytes are the weights read (every projection, norm and lm_head; 32
+    embedding rows) plus the cached K/V rows and GDN states the step reads. The golden decoder's
+    step (the whole two-stream forward over prompt + block) is timed beside it."""
+    import torch
+    from torch import nn
+
+    from dllm_qwen38_amd import blockdiff, decode
+    from dllm_qwen38_amd import model as hybrid
+
+    P, block = 2048, 32
+    dev = torch.device("cuda:0")
+    c = hybrid.config_27b_truncated(layers=16)
+    model, lm_head = hybrid.build(c, device=dev, dtype=torch.bfloat16, seed=513)
+    model.requires_grad_(False)
+    lm_head.requires_grad_(False)
+    g = torch.Generator().manual_seed(511)
+    x0 = torch.randint(0, c.vocab_size, (1, P + block), generator=g)
+    xt = x0.clone()
+    xt[:, P + 3:] = c.vocab_size - 1  # a block with 3 tokens committed, 29 still masked
+    x0, xt = x0.to(dev), xt.to(dev)
+    stream = torch.cuda.current_stream(dev)
+    cache = decode.PrefixCache(model, batch=1, capacity=P + block, block=block)
+
+    def prefill():
+        cache.reset()
+        decode.forward_segment(model, lm_head, cache, x0[:, :P], commit=True, logits=False)
+
+    prefill_ms, _ = _timed(prefill, 2, 1, stream)
+
+    def step():
+        decode.forward_segment(model, lm_head, cache, xt[:, P:], commit=False)
+
+    steps, warm = max(1, a.steps), max(1, a.warmup)
+    ms, wall = _timed(step, steps, warm, stream)
+
+    def golden():
+        with torch.inference_mode():
+            blockdiff.block_diffusion_forward(model, lm_head, x0, xt, block)
+
+    golden_ms, _ = _timed(golden, 2, 1, stream)
+
+    esz = 2
+    wbytes = sum(m.weight.numel() * m.weight.element_size() for m in model.modules()
+                 if isinstance(m, nn.Linear)) + lm_head.weight.numel() * esz
+    wbytes += sum(p.numel() * p.element_size() for n, p in model.named_parameters()
+                  if not n.startswith("embed_tokens") and p.dim() == 1)  # norms, conv bias, decay
+    wbytes += sum(m.conv1d.weight.numel() * m.conv1d.weight.element_size() for m in model.modules()
+                  if hasattr(m, "conv1d"))
+    wbytes += block * c.hidden_size * esz  # embedding rows
+    kv = sum(2 * t[:, : P + block].numel() * esz for t in cache.k.values())
+    st = sum(s.numel() * 4 for s in cache.state.values() if s is not None)
+    total = wbytes + kv + st
+    gbs = total / (ms * 1e-3) / 1e9
+    res = {
+        "metric": "cached denoising step of the block-diffusion decoder: block forwards/s (32-token block over "
+                  "a 2048-token clean prefix), 16-layer 27B-class stack; % HBM roofline",
+        "value": 1e3 / ms, "unit": "forwards/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, uniform ids, 29 of 32 block positions masked)",
+        "config": {"workload": "prefix-cached denoising step, 16 layers (12 GDN + 4 attention) hidden 5120 "
+                               "MLP 17408 vocab 151936, B=1, prefix 2048, block 32, logits of the block",
+                   "global_batch": 1, "seq_len": P + block, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+        "algorithmic_bytes": total, "weight_bytes": wbytes, "kv_cache_bytes": kv, "state_bytes": st,
+        "prefill_ms": prefill_ms, "golden_step_ms": golden_ms, "speedup_vs_golden_step": golden_ms / ms,
+        "cache_bytes": cache.nbytes(), "wall_s_timed": wall, "cpu_baseline": None,
     }
     print(json.dumps(res))
     return 0

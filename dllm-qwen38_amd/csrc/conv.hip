@@ -216,7 +216,10 @@ extern "C" int dllm_causal_conv1d_fwd(const void* x, const int64_t* x_strides, c
     return fail(DLLM_EINVAL, "causal_conv1d: bad sizes B=%d C=%d T=%d K=%d", B, C, T, width);
   if (prefix_len < 0 || (prefix_len > 0 && (!prefix || !prefix_strides)))
     return fail(DLLM_EINVAL, "causal_conv1d: bad prefix");
-  const int seg = 64;
+  // positions per thread: halved until the grid has enough workgroups to fill the chip, so a short
+  // segment (a decoding step of one block) still spreads over every CU
+  int seg = 64;
+  while (seg > 1 && (long long)((C + 255) / 256) * B * ((T + seg - 1) / seg) < 2048) seg >>= 1;
   dim3 grid((C + 255) / 256, (T + seg - 1) / seg, B);
   if (grid.y > 65535 || grid.z > 65535) return fail(DLLM_EUNSUPPORTED, "causal_conv1d: grid too large");
   hipStream_t st = (hipStream_t)stream;

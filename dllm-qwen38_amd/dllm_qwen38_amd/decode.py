@@ -23,8 +23,8 @@ from dataclasses import dataclass, field
 
 import torch
 
-from . import attention, gdn, norms
-from .blockdiff import FULL, LINEAR, _eps, block_diffusion_forward, mlp, rmsnorm, rotary_tables
+from . import _lib, attention, gdn, norms
+from .blockdiff import FULL, LINEAR, _eps, block_diffusion_forward, rmsnorm, rotary_tables
 
 
 @dataclass
@@ -108,6 +108,53 @@ def generate(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int, block
     return trace
 
 
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., K] @ weight[N, K]^T for the few token rows of a decoding step (bf16, at most 64 rows,
+    K a multiple of 64) on the HIP kernel that streams the weight into MFMA operands; fp32
+    accumulation, deterministic. Returns [..., N] bf16."""
+    dev = _lib.require_device(x, weight)
+    K = x.shape[-1]
+    N = weight.shape[0]
+    if weight.dim() != 2 or weight.shape[1] != K:
+        raise ValueError(f"weight must be [N, {K}], got {tuple(weight.shape)}")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("decode_linear takes bf16 x and weight")
+    x2 = x.reshape(-1, K).contiguous()
+    w = weight.contiguous()
+    M = x2.shape[0]
+    L = _lib.lib()
+    splits = L.dllm_decode_linear_splits(M, N, K)
+    if splits <= 0 or M > 64:
+        raise ValueError(f"decode_linear does not take M={M} N={N} K={K} (M <= 64, K % 64 == 0)")
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev) if out is None else out
+    if tuple(y.shape) != (M, N) or not y.is_contiguous() or y.dtype != torch.bfloat16:
+        raise ValueError("out must be a contiguous bf16 [M, N] tensor")
+    ws = torch.empty(splits * M * N, dtype=torch.float32, device=dev) if splits > 1 else None
+    _lib.check(L.dllm_decode_linear_fwd(x2.data_ptr(), w.data_ptr(), y.data_ptr(), _lib.ptr(ws), M, N, K, splits,
+                                        _lib.dtype_code(x.dtype), _lib.stream_handle(dev)), "dllm_decode_linear_fwd")
+    return y.reshape(*x.shape[:-1], N)
+
+
+def _proj(lin, x: torch.Tensor) -> torch.Tensor:
+    """nn.Linear `lin` on x. For a block of bf16 rows the decoding-step kernel takes the narrow
+    projections (N <= 2048: the per-head gates, k and v, where the library GEMM pays a fixed ~19 us)
+    and the deep ones (K >= 12288: the MLP down projection); the library GEMM keeps the wide ones,
+    where it streams the weights faster, and the many rows of a prefill (and fp32 or biased
+    projections)."""
+    w = lin.weight
+    rows = x.numel() // x.shape[-1]
+    N, K = w.shape
+    if (lin.bias is None and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and rows <= 64
+            and K % 64 == 0 and (N <= 2048 or K >= 12288)):
+        return decode_linear(x, w)
+    return lin(x)
+
+
+def _mlp(m, x: torch.Tensor) -> torch.Tensor:
+    """SwiGLU MLP ([hf]:704-717) with the decoding-step projections."""
+    return _proj(m.down_proj, norms.swiglu(_proj(m.gate_proj, x), _proj(m.up_proj, x)))
+
+
 class PrefixCache:
     """Per-layer state of a committed clean prefix, resident in HBM, for `forward_segment`.
 
@@ -162,9 +209,9 @@ def _gdn_segment(m, x: torch.Tensor, cache: PrefixCache, i: int, commit: bool) -
     prefix's last projections in, the recurrence starts from the prefix state; with commit, the
     state after the segment and its last projections replace the cached ones."""
     B, T, _ = x.shape
-    raw = m.in_proj_qkv(x)  # [B, T, conv_dim]
-    z = m.in_proj_z(x)
-    beta, g = gdn._beta_g(m, m.in_proj_b(x), m.in_proj_a(x))
+    raw = _proj(m.in_proj_qkv, x)  # [B, T, conv_dim]
+    z = _proj(m.in_proj_z, x)
+    beta, g = gdn._beta_g(m, _proj(m.in_proj_b, x), _proj(m.in_proj_a, x))
     mixed = gdn.causal_conv1d_fn(raw.transpose(1, 2), m.conv1d.weight.squeeze(1), m.conv1d.bias,
                                  activation=m.activation, conv_prefix=cache.conv[i]).transpose(1, 2)
     q, k, v = gdn._split_qkv(mixed, m, B, T)
@@ -179,7 +226,7 @@ def _gdn_segment(m, x: torch.Tensor, cache: PrefixCache, i: int, commit: bool) -
         cache.state[i] = states[:, -1].contiguous()
     Dv = m.head_v_dim
     o = norms.gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm.weight, _eps(m.norm))
-    return m.out_proj(o.reshape(B, T, -1))
+    return _proj(m.out_proj, o.reshape(B, T, -1))
 
 
 def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: int) -> torch.Tensor:
@@ -188,15 +235,15 @@ def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: i
     block-causal attention against cache rows 0..pos0+T-1, sigmoid gate, o_proj."""
     B, T, _ = x.shape
     hd = att.head_dim
-    q, gate = torch.chunk(att.q_proj(x).view(B, T, -1, 2 * hd), 2, dim=-1)
+    q, gate = torch.chunk(_proj(att.q_proj, x).view(B, T, -1, 2 * hd), 2, dim=-1)
     gate = gate.reshape(B, T, -1)
     cos, sin = cache.cos[pos0:pos0 + T], cache.sin[pos0:pos0 + T]
-    q, k = norms.qk_norm_rope(q, att.k_proj(x).view(B, T, -1, hd), att.q_norm, att.k_norm, cos, sin, T)
+    q, k = norms.qk_norm_rope(q, _proj(att.k_proj, x).view(B, T, -1, hd), att.q_norm, att.k_norm, cos, sin, T)
     cache.k[i][:, pos0:pos0 + T] = k
-    cache.v[i][:, pos0:pos0 + T] = att.v_proj(x).view(B, T, -1, hd)
+    cache.v[i][:, pos0:pos0 + T] = _proj(att.v_proj, x).view(B, T, -1, hd)
     o = attention.block_causal_attention(q, cache.k[i][:, :pos0 + T], cache.v[i][:, :pos0 + T], block=cache.block,
                                          q_offset=pos0, scale=float(att.scaling))
-    return att.o_proj(o.reshape(B, T, -1) * torch.sigmoid(gate))
+    return _proj(att.o_proj, o.reshape(B, T, -1) * torch.sigmoid(gate))
 
 
 @torch.no_grad()
@@ -228,12 +275,12 @@ def forward_segment(text_model, lm_head, cache: PrefixCache, ids: torch.Tensor, 
         else:
             o = _attention_segment(layer.self_attn, x, cache, i, P)
         x, h = rmsnorm(o, layer.post_attention_layernorm, residual=h)
-        pending = mlp(layer.mlp, x)
+        pending = _mlp(layer.mlp, x)
     if commit:
         cache.length = P + T
     if not logits:
         return None
-    return lm_head(rmsnorm(pending, text_model.norm, residual=h)[0])
+    return _proj(lm_head, rmsnorm(pending, text_model.norm, residual=h)[0])
 
 
 @torch.no_grad()

@@ -139,6 +139,20 @@ int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, con
                                     int Hq, int Hkv, int d, int block, float scale, int dtype, void* stream);
 
 /*
+ * Projections of a decoding step (few token rows): y[M,N] = x[M,K] W[N,K]^T, bf16 in and out, fp32
+ * accumulation; M <= 64, K a multiple of 64, x and W row-major and 16-byte aligned, y [M,N]
+ * contiguous. Replaces the nn.Linear calls (in_proj_*, q/k/v/o_proj, the MLP, lm_head) that every
+ * denoising step of the reference decoder runs inside block_diffusion_forward
+ * (src/dllm_qwen38/decode.py:63-66; [hf]:168-184,656-717) when they see one block of tokens.
+ * splits > 1 splits K over workgroups; then workspace holds splits*M*N floats and a second launch
+ * sums the splits in order (deterministic). dllm_decode_linear_splits(M, N, K) gives the split count
+ * that fills the chip (0 if the shape is not taken).
+ */
+int dllm_decode_linear_splits(int M, int N, int K);
+int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, float* workspace, int M, int N, int K,
+                           int splits, int dtype, void* stream);
+
+/*
  * Qwen3.5 RMSNorm over the last dim of x [rows, dim]: y = x * rsqrt(mean(x^2) + eps) * (1 + w)
  * in fp32 (unit_offset = 1; 0 applies w as is), rounded once to x's dtype.
  * Replaces [hf]:720-737 Qwen3_5RMSNorm as called by the decoder layer and the final norm

@@ -59,3 +59,16 @@ def test_the_hip_path_fails_loudly_on_host_tensors(tiny):
 def test_trace_tokens_per_forward():
     t = decode.DecodeTrace(tokens=[1, 2], forwards=4, generated=10)
     assert t.tokens_per_forward == 2.5 and decode.DecodeTrace(tokens=[]).tokens_per_forward == 0.0
+
+
+def test_decode_linear_split_rule_and_host_errors():
+    from dllm_qwen38_amd import _lib
+
+    L = _lib.lib()
+    assert L.dllm_decode_linear_splits(32, 100, 100) == 0  # K not a multiple of 64
+    assert L.dllm_decode_linear_splits(32, 151936, 5120) == 1  # 4748 feature tiles fill the chip alone
+    s = L.dllm_decode_linear_splits(32, 5120, 5120)
+    assert 1 < s <= 8
+    assert L.dllm_decode_linear_splits(32, 48, 5120) == 8
+    with pytest.raises(RuntimeError):
+        decode.decode_linear(torch.zeros(32, 64, dtype=torch.bfloat16), torch.zeros(8, 64, dtype=torch.bfloat16))

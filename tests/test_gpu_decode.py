@@ -83,6 +83,26 @@ def test_27b_class_decoding_step_attention(dev):
     _check_att(got, ref, torch.bfloat16, v.float().abs().max().item(), "27b step")
 
 
+@pytest.mark.parametrize("M,N,K", [(32, 5120, 5120), (32, 17408, 5120), (32, 5120, 17408), (32, 48, 5120),
+                                   (1, 100, 64), (7, 300, 320), (33, 1000, 640), (64, 96, 6144)])
+def test_decode_linear_matches_fp32_reference(dev, M, N, K):
+    """y = x W^T against torch fp32 on the same bf16 inputs: within the bf16 rounding of the output
+    (2^-8 relative) plus 2^-16 of sum|x||w| for the accumulation order."""
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    got = decode.decode_linear(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float().T
+    scale = x.float().abs() @ w.float().abs().T
+    err = (got.float().cpu() - ref).abs()
+    print(f"M{M} N{N} K{K} splits {decode._lib.lib().dllm_decode_linear_splits(M, N, K)}: max|d|={err.max():.3e}")
+    assert (err <= 2 ** -8 * ref.abs() + 2 ** -16 * scale).all()
+    again = decode.decode_linear(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(got, again), "split-K sums must be deterministic"
+
+
 @pytest.fixture(scope="module")
 def tiny(dev):
     cpu_model, cpu_head = tiny_hf_model(seed=0)

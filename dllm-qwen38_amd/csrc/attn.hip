@@ -376,8 +376,8 @@ static int launch_attn(const AttnArgs& a, hipStream_t st) {
 // runs two waves per SIMD. (Splitting S between the pair instead needs an LDS exchange and a second
 // barrier per tile, which measured slower than computing S twice.)
 // K and V tiles travel global -> LDS by direct loads, no registers: each wave instruction moves
-// 1 KB = 64 lanes x 16 bytes; rows are dense with their 16-byte chunks XOR-swizzled by row so that
-// the K fragment reads and the V^T transpose reads are free of bank conflicts. A ring of NST
+// 1 KB = 64 lanes x 16 bytes; rows are dense with their 16-byte chunks XOR-swizzled (swz_key) so
+// that the K fragment reads and the V^T transpose reads are free of bank conflicts. A ring of NST
 // stages keeps NST - 1 tiles in flight ahead of the one being computed; one barrier per tile.
 // ---------------------------------------------------------------------------------------------
 template <int D>
@@ -388,10 +388,24 @@ struct DmaSmem {
   static constexpr int TOTAL = NST * STAGE;
 };
 
+// Chunk swizzle of a tile row: logical 16-byte chunk c of row r sits at physical chunk c ^ swz_key(r).
+// LDS has 64 banks of 4 bytes; a 16-byte read is served 16 lanes per pass and an 8-byte read 32
+// lanes per pass. The K fragment reads take one chunk of 16 consecutive rows per pass, so the key
+// must be a bijection of the row's low bits; the V^T transpose reads take four chunks of each of
+// four consecutive rows per pass, so the key must also put the row's lowest two bits above the
+// chunk's lowest two. Swapping the row's two 2-bit fields does both for D = 128 and 256 (measured
+// 4% and 8% faster than keying by the row alone). D = 64 keeps the plain row key, which measured
+// faster there.
+template <int D>
+__device__ __forceinline__ int swz_key(int row) {
+  constexpr int CH = D / 8;
+  if constexpr (CH >= 16) return ((row & 3) << 2) | ((row >> 2) & 3);
+  else return row & (CH - 1);
+}
+
 template <int D>
 __device__ __forceinline__ int swz_off(int row, int col) {  // byte offset of (row, col) in a swizzled tile
-  constexpr int CH = D / 8;
-  return row * (2 * D) + (((col >> 3) ^ (row & (CH - 1))) << 4) + ((col & 7) << 1);
+  return row * (2 * D) + (((col >> 3) ^ swz_key<D>(row)) << 4) + ((col & 7) << 1);
 }
 
 // s_waitcnt with vmcnt(N) and the other counters unconstrained (gfx9 encoding)
@@ -498,7 +512,7 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
       const bool isv = gi >= IPT;
       const int row0 = (gi % IPT) * RPI;
       const int row = row0 + lane / CH;
-      const int chunk = (lane % CH) ^ (row & (CH - 1));
+      const int chunk = (lane % CH) ^ swz_key<D>(row);
       const int key = min(j0 + row, Lk - 1);  // rows past the end load a valid row; they are masked
       const long long off = (long long)((BC ? 0 : kh * L) + key) * (isv ? a.v_st : a.k_st) + chunk * 8;
       const bf16* src = (isv ? vbase : kbase) + off;

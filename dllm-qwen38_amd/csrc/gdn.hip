@@ -9,9 +9,9 @@
 // Per tile and stream:
 //   load    q, k (key head hv / (Hv/Hk): GQA by indexing, no expansion), v, beta, g from the
 //           registers prefetched during the previous tile, raw into LDS (bf16: all row-major;
-//           the transposed operands come from LDS transpose reads); q row norms (DPP
+//           the transposed operands come from LDS transpose reads); q and k row norms (DPP
 //           reductions); gamma = inclusive scan of g over the tile (DPP).
-//   G       K K^T and Q K^T on MFMA (k norms from the Gram diagonal); decay/beta masks -> A
+//   G       K K^T and Q K^T on MFMA; decay/beta masks -> A
 //           (fp32), P with the q norms and Dk^-1/2 folded in.
 //   T       T = (I + A)^-1 in fp32 by a blocked inverse inside the wave that produced A: 8x8
 //           diagonal blocks by forward substitution, then the 8x8 and the 16x16 off-diagonal
@@ -336,15 +336,22 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
           VT[(ve1 + i) * TROW + lr] = xv[(NV / 2 + i) / EPV][(NV / 2 + i) % EPV];
         }
       }
-      // q row norm (the k norms come from the diagonal of K K^T)
-      float ss = 0.f;
+      // q and k row norms: fp32 sums of squares of the row (DPP reductions over its 8 threads),
+      // as the reference's l2norm; the G phase then needs no round trip for them
+      float ss = 0.f, sk = 0.f;
 #pragma unroll
       for (int i = 0; i < NE; ++i) {
         const float x = to_f32(xq[i / EPV][i % EPV]);
+        const float y = to_f32(xk[i / EPV][i % EPV]);
         ss = __builtin_fmaf(x, x, ss);
+        sk = __builtin_fmaf(y, y, sk);
       }
       ss = dpp_sum8(ss);
-      if (lseg == 0) RNQ[lr] = a.l2norm ? a.scale * rsqrtf(ss + 1e-6f) : a.scale;
+      sk = dpp_sum8(sk);
+      if (lseg == 0) {
+        RNQ[lr] = a.l2norm ? a.scale * rsqrtf(ss + 1e-6f) : a.scale;
+        RNK[lr] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
+      }
       // beta, g and the cumulative decay (inclusive scan over the tile's rows), one wave per set:
       // lanes 0..31 hold g of rows 0..31 (zero for padding rows and for lanes 32..63); scan
       // within each 16-lane DPP row, then carry row 0's total into row 1 (row_bcast:15)
@@ -382,7 +389,7 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
     // ------------------------------------------------------------------ G phase + diagonal blocks of T
     // (every step issues all of its LDS reads before computing: one LDS round trip per step)
     {
-      // K K^T (+ k norms, A, and the first two levels of T) on waves 0 / 5, Q K^T on waves 2 / 7:
+      // K K^T (+ A and the blocked inverse T) on waves 0 / 5, Q K^T on waves 2 / 7:
       // four different SIMDs in fork mode
       const bool isG = (u == (set == 0 ? 0 : 1));
       const bool isQK = (u == (set == 0 ? 2 : 3));
@@ -416,12 +423,6 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
         }
         const float gj = GAML[l32];
         if (isG) {
-          // k norms from the diagonal of K K^T: lane (j, h = (j>>2)&1) holds element (j, j)
-          float dg = 0.f;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) dg = (rho(v, ho) == lo) ? acc[v] : dg;
-          if (h == ((l32 >> 2) & 1)) RNK[l32] = a.l2norm ? rsqrtf(dg + 1e-6f) : 1.f;
-          wave_lds_sync();
           f32x4 bet4[4], rnk4[4];
 #pragma unroll
           for (int m = 0; m < 4; ++m) {

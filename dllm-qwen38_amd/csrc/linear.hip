@@ -3,83 +3,114 @@
 //
 // A cached denoising step runs every projection of the stack on one block of tokens (32 rows), so
 // each weight is read once for 32 rows and the step is bound by streaming the weights from HBM.
-// The library GEMMs stream the wide projections well, but a narrow one (the per-head gates, the
-// attention k and v: N <= 2048) costs them a fixed ~19 us, and a deep one (the MLP down
-// projection, K = 17408) runs at ~2.2 TB/s; this kernel takes those. The weights stream straight
-// into MFMA operands:
-//   * a workgroup owns 32 output features (one 32x32 accumulator tile) and a range of K; its four
-//     waves split that range; per step of 64 k a lane loads 64 contiguous bytes of one weight row
-//     (B operand, lane = feature) and of one token row (A operand, lane = token; the token rows
-//     are small and stay in L2), and issues four v_mfma_f32_32x32x16_bf16. Lane (row, h) carries
-//     k = 32h + 8u + 0..7 in MFMA u for both operands, so the contraction is exact in any order;
-//   * the four waves' tiles are summed through LDS in a fixed order; with one K range the sum is
-//     rounded to bf16 and stored, otherwise fp32 partials [S, M, N] go to a workspace and a second
-//     kernel sums them in split order. Results are deterministic run to run.
+// The weights stream through LDS in wide coalesced reads:
+//   * a workgroup owns 128 output features (four 32x32 accumulator tiles, one per wave) and a
+//     range of K. Per step of 64 k it stages the weight tile [128 features x 64 k] and the token
+//     tile [32 rows x 64 k] with direct global -> LDS loads (each wave instruction moves 1 KB: eight
+//     whole 128-byte row segments, no registers), in a ring of LIN_NST stages that keeps
+//     LIN_NST - 1 steps in flight;
+//   * rows are 128 bytes with their 16-byte chunks XOR-swizzled by (row >> 1), so the operand reads
+//     (16 rows of one chunk per pass) touch every bank once;
+//   * wave w reads the B operand (lane = feature) of its 32 features and the A operand (lane =
+//     token) from LDS, 16 bytes each, and issues four v_mfma_f32_32x32x16_bf16 per step (lane
+//     (row, h) carries k = 16u + 8h + 0..7 in MFMA u for both operands);
+//   * with one K range the tile is rounded to bf16 and stored; with several, fp32 partials
+//     [S, M, N] go to a workspace and a second kernel sums them in split order (deterministic);
 //   * more than 32 token rows: grid.z takes the next 32 rows (the weights are streamed again).
 #include "common.h"
 
 namespace dllm {
 
-constexpr int LIN_UNROLL = 2;  // 64-k steps per loop iteration: 8 x 16-byte loads in flight per operand
+constexpr int LIN_NST = 3;                 // ring stages
+constexpr int LIN_W_BYTES = 128 * 64 * 2;  // weight tile of one step
+constexpr int LIN_X_BYTES = 32 * 64 * 2;   // token tile of one step
+constexpr int LIN_STAGE = LIN_W_BYTES + LIN_X_BYTES;
+
+__device__ __forceinline__ int lin_off(int row, int chunk) {  // byte offset of a 16-byte chunk of a 128-byte row
+  return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+template <int N>
+__device__ __forceinline__ void lin_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
 
 __global__ __launch_bounds__(256) void decode_linear_kernel(const bf16* __restrict__ x, const bf16* __restrict__ w,
                                                            bf16* __restrict__ y, float* __restrict__ part, int M, int N,
                                                            int K, int kchunk) {
-  __shared__ __attribute__((aligned(16))) float red[4][16][64];  // [wave][value][lane]
+  __shared__ __attribute__((aligned(16))) unsigned char smem[LIN_NST * LIN_STAGE];
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int tile = blockIdx.x, split = blockIdx.y, m0 = blockIdx.z * 32;
-  const int n = tile * 32 + l32;
-  const int m = m0 + l32;
-  const bool nok = n < N, mok = m < M;
-  const bf16* wr = w + (long long)(nok ? n : N - 1) * K;
-  const bf16* xr = x + (long long)(mok ? m : 0) * K;
-  const int kq = kchunk / 4;                       // this wave's share, a multiple of 64
-  const int kb = split * kchunk + wave * kq;
-  const int ke = min(K, kb + kq);
+  const int n0 = tile * 128;
+  const int kb = split * kchunk;
+  const int ke = min(K, kb + kchunk);
+  const int nsteps = ke > kb ? (ke - kb) / 64 : 0;  // K and kchunk are multiples of 64
+
+  // staging role of this lane: row 8 i + lane / 8 of its rows, logical chunk (lane % 8) ^ key(row)
+  const int srow = lane >> 3, schunk = lane & 7;
+  auto stage = [&](int s) {
+    unsigned char* sb = smem + (s % LIN_NST) * LIN_STAGE;
+    const int k0 = kb + 64 * s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // this wave's 4 of the 16 weight instructions: rows 32 wave + 8 i ..
+      const int row = 32 * wave + 8 * i + srow;
+      const int n = min(n0 + row, N - 1);  // rows past N load a valid row; their outputs are not stored
+      const int c = schunk ^ ((row >> 1) & 7);
+      const bf16* src = w + (long long)n * K + k0 + 8 * c;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(sb + (32 * wave + 8 * i) * 128), 16,
+                                       0, 0);
+    }
+    {  // token tile: wave w stages rows 8 w .. 8 w + 7
+      const int row = 8 * wave + srow;
+      const int m = min(m0 + row, M - 1);
+      const int c = schunk ^ ((row >> 1) & 7);
+      const bf16* src = x + (long long)m * K + k0 + 8 * c;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(sb + LIN_W_BYTES + 8 * wave * 128), 16,
+                                       0, 0);
+    }
+  };
+  constexpr int PER = 5;  // direct loads per wave per step
+  static_assert(LIN_NST == 3, "wait_step assumes at most one step in flight behind the waited one");
+  auto wait_step = [&](int s) {  // step s has landed for this wave (step s + 1 may still travel)
+    if (s + 1 < nsteps) lin_wait_vmcnt<PER>();
+    else lin_wait_vmcnt<0>();
+  };
+
   f32x16 acc = zero16();
-  const bf16x8 z8 = {};
-  int k0 = kb;
-  for (; k0 + 64 * LIN_UNROLL <= ke; k0 += 64 * LIN_UNROLL) {
-    bf16x8 wv[LIN_UNROLL][4], xv[LIN_UNROLL][4];
 #pragma unroll
-    for (int s = 0; s < LIN_UNROLL; ++s)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        wv[s][u] = *(const bf16x8*)(wr + k0 + 64 * s + 32 * h + 8 * u);
-        xv[s][u] = mok ? *(const bf16x8*)(xr + k0 + 64 * s + 32 * h + 8 * u) : z8;
-      }
-#pragma unroll
-    for (int s = 0; s < LIN_UNROLL; ++s)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xv[s][u], wv[s][u], acc, 0, 0, 0);
-  }
-  for (; k0 < ke; k0 += 64) {  // K is a multiple of 64
-    bf16x8 wv[4], xv[4];
+  for (int s = 0; s < LIN_NST - 1; ++s)
+    if (s < nsteps) stage(s);
+  if (nsteps > 0) wait_step(0);
+  __syncthreads();
+  for (int s = 0; s < nsteps; ++s) {
+    if (s + LIN_NST - 1 < nsteps) stage(s + LIN_NST - 1);  // its stage held step s - 1, done before the barrier
+    const unsigned char* sb = smem + (s % LIN_NST) * LIN_STAGE;
+    const unsigned char* xs = sb + LIN_W_BYTES;
+    bf16x8 a[4], bv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      wv[u] = *(const bf16x8*)(wr + k0 + 32 * h + 8 * u);
-      xv[u] = mok ? *(const bf16x8*)(xr + k0 + 32 * h + 8 * u) : z8;
+      a[u] = *(const bf16x8*)(xs + lin_off(l32, 2 * u + h));
+      bv[u] = *(const bf16x8*)(sb + lin_off(32 * wave + l32, 2 * u + h));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xv[u], wv[u], acc, 0, 0, 0);
+    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[u], bv[u], acc, 0, 0, 0);
+    if (s + 1 < nsteps) wait_step(s + 1);
+    __syncthreads();  // step s + 1 staged by every wave; every wave is done with step s's stage
   }
-  // acc: lane holds feature column l32, token rows rho(v, h); sum the four waves in wave order
+  // acc: lane holds feature column l32 of this wave's tile, token rows rho(v, h)
+  const int n = n0 + 32 * wave + l32;
+  if (n >= N) return;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) red[wave][v][lane] = acc[v];
-  __syncthreads();
-  // thread -> (lane ln, values 4g .. 4g+3): token rows 8g + 4hh + 0..3, feature ln % 32
-  const int ln = tid & 63, g = tid >> 6, hh = ln >> 5;
-  const int nn = tile * 32 + (ln & 31);
-  if (nn >= N) return;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int v = 4 * g + e;
-    const float sum = ((red[0][v][ln] + red[1][v][ln]) + red[2][v][ln]) + red[3][v][ln];
-    const int mm = m0 + 8 * g + 4 * hh + e;
-    if (mm >= M) continue;
-    if (part) part[((long long)split * M + mm) * N + nn] = sum;
-    else y[(long long)mm * N + nn] = (bf16)sum;
+  for (int v = 0; v < 16; ++v) {
+    const int m = m0 + rho(v, h);
+    if (m >= M) continue;
+    if (part) part[((long long)split * M + m) * N + n] = acc[v];
+    else y[(long long)m * N + n] = (bf16)acc[v];
   }
 }
 
@@ -99,10 +130,9 @@ using namespace dllm;
 
 extern "C" int dllm_decode_linear_splits(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
-  const long long tiles = (long long)((N + 31) / 32) * ((M + 31) / 32);
-  // about two workgroups per CU, each K range at least 256 deep and at most 8 splits (measured: more
-  // splits cost more in partial sums than they gain in parallelism)
-  long long s = (512 + tiles - 1) / tiles;
+  const long long tiles = (long long)((N + 127) / 128) * ((M + 31) / 32);
+  // about 1.5 workgroups per CU, each K range at least 256 deep and at most 8 splits
+  long long s = (384 + tiles - 1) / tiles;
   long long smax = K / 256 > 0 ? K / 256 : 1;
   if (smax > 8) smax = 8;
   if (s > smax) s = smax;
@@ -119,13 +149,13 @@ extern "C" int dllm_decode_linear_fwd(const void* x, const void* weight, void* y
   if (M > 64) return fail(DLLM_EUNSUPPORTED, "decode linear: M=%d > 64 rows (use a library GEMM)", M);
   if (((uintptr_t)x | (uintptr_t)weight) & 15) return fail(DLLM_EINVAL, "decode linear: x and weight must be 16-byte aligned");
   if (splits > 1 && !workspace) return fail(DLLM_EINVAL, "decode linear: %d splits need a workspace", splits);
-  // K range per split: a multiple of 256 (four waves of 64-k steps)
-  const int kchunk = ((K + splits - 1) / splits + 255) / 256 * 256;
+  // K range per split: a multiple of 64 (one staged step)
+  const int kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;
   const int S = (K + kchunk - 1) / kchunk;
-  const unsigned tiles = (unsigned)((N + 31) / 32);
-  if (tiles > 0x7fffffffu) return fail(DLLM_EUNSUPPORTED, "decode linear: grid too large");
+  const long long tiles = (N + 127) / 128;
+  if (tiles > 0x7fffffffLL) return fail(DLLM_EUNSUPPORTED, "decode linear: grid too large");
   hipStream_t st = (hipStream_t)stream;
-  decode_linear_kernel<<<dim3(tiles, S, (M + 31) / 32), 256, 0, st>>>(
+  decode_linear_kernel<<<dim3((unsigned)tiles, S, (M + 31) / 32), 256, 0, st>>>(
       (const bf16*)x, (const bf16*)weight, (bf16*)y, S > 1 ? workspace : nullptr, M, N, K, kchunk);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear launch: %s", hipGetErrorString(e));

@@ -136,16 +136,12 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | 
 
 
 def _proj(lin, x: torch.Tensor) -> torch.Tensor:
-    """nn.Linear `lin` on x. For a block of bf16 rows the decoding-step kernel takes the narrow
-    projections (N <= 2048: the per-head gates, k and v, where the library GEMM pays a fixed ~19 us)
-    and the deep ones (K >= 12288: the MLP down projection); the library GEMM keeps the wide ones,
-    where it streams the weights faster, and the many rows of a prefill (and fp32 or biased
-    projections)."""
+    """nn.Linear `lin` on x: the decoding-step kernel for a block of bf16 rows (at most 64), the
+    library GEMM for the many rows of a prefill and for fp32 or biased projections."""
     w = lin.weight
     rows = x.numel() // x.shape[-1]
-    N, K = w.shape
     if (lin.bias is None and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and rows <= 64
-            and K % 64 == 0 and (N <= 2048 or K >= 12288)):
+            and w.shape[1] % 64 == 0):
         return decode_linear(x, w)
     return lin(x)
 

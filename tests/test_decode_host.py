@@ -66,9 +66,10 @@ def test_decode_linear_split_rule_and_host_errors():
 
     L = _lib.lib()
     assert L.dllm_decode_linear_splits(32, 100, 100) == 0  # K not a multiple of 64
-    assert L.dllm_decode_linear_splits(32, 151936, 5120) == 1  # 4748 feature tiles fill the chip alone
+    assert L.dllm_decode_linear_splits(32, 151936, 5120) == 1  # 1187 feature tiles fill the chip alone
     s = L.dllm_decode_linear_splits(32, 5120, 5120)
     assert 1 < s <= 8
     assert L.dllm_decode_linear_splits(32, 48, 5120) == 8
+    assert L.dllm_decode_linear_splits(32, 151936, 5120) == 1
     with pytest.raises(RuntimeError):
         decode.decode_linear(torch.zeros(32, 64, dtype=torch.bfloat16), torch.zeros(8, 64, dtype=torch.bfloat16))

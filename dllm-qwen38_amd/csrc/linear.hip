@@ -16,7 +16,11 @@
 //     (row, h) carries k = 16u + 8h + 0..7 in MFMA u for both operands);
 //   * with one K range the tile is rounded to bf16 and stored; with several, fp32 partials
 //     [S, M, N] go to a workspace and a second kernel sums them in split order (deterministic);
-//   * more than 32 token rows: grid.z takes the next 32 rows (the weights are streamed again).
+//   * more than 32 token rows: grid.z takes the next 32 rows (the weights are streamed again);
+//   * up to four projections of the same x (q | k | v, the four mixer inputs, gate | up) share one
+//     launch and one split reduction: the grid's tiles run through the weights in turn. With the
+//     SwiGLU epilogue (gate | up) the reduction writes round(round(silu(gate)) * up), the MLP's
+//     activation, instead of the two projections.
 #include "common.h"
 
 namespace dllm {
@@ -36,14 +40,36 @@ __device__ __forceinline__ void lin_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-__global__ __launch_bounds__(256) void decode_linear_kernel(const bf16* __restrict__ x, const bf16* __restrict__ w,
-                                                           bf16* __restrict__ y, float* __restrict__ part, int M, int N,
-                                                           int K, int kchunk) {
+constexpr int LIN_MAXSEG = 4;
+struct LinSeg {
+  const bf16* w;  // [N, K]
+  bf16* y;        // [M, N]
+  float* part;    // [S, M, N] fp32 partials (split path)
+  int N;
+  int tile0;      // first grid tile of this projection
+  long long e0;   // first element of this projection in the reduction's index space
+};
+struct LinArgs {
+  const bf16* x;
+  LinSeg seg[LIN_MAXSEG];
+  int nseg, M, K, kchunk, S, split_path, swiglu;
+};
+
+__global__ __launch_bounds__(256) void decode_linear_kernel(LinArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[LIN_NST * LIN_STAGE];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-  const int tile = blockIdx.x, split = blockIdx.y, m0 = blockIdx.z * 32;
+  const int split = blockIdx.y, m0 = blockIdx.z * 32;
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < LIN_MAXSEG; ++i)
+    if (i < a.nseg && (int)blockIdx.x >= a.seg[i].tile0) si = i;
+  const LinSeg& sg = a.seg[si];
+  const bf16* __restrict__ const x = a.x;
+  const bf16* __restrict__ const w = sg.w;
+  const int M = a.M, N = sg.N, K = a.K, kchunk = a.kchunk;
+  const int tile = blockIdx.x - sg.tile0;
   const int n0 = tile * 128;
   const int kb = split * kchunk;
   const int ke = min(K, kb + kchunk);
@@ -109,19 +135,34 @@ __global__ __launch_bounds__(256) void decode_linear_kernel(const bf16* __restri
   for (int v = 0; v < 16; ++v) {
     const int m = m0 + rho(v, h);
     if (m >= M) continue;
-    if (part) part[((long long)split * M + m) * N + n] = acc[v];
-    else y[(long long)m * N + n] = (bf16)acc[v];
+    if (a.split_path) sg.part[((long long)split * M + m) * N + n] = acc[v];
+    else sg.y[(long long)m * N + n] = (bf16)acc[v];
   }
 }
 
-// y = bf16(sum over splits of part[s]) in split order
-__global__ __launch_bounds__(256) void decode_linear_reduce_kernel(const float* __restrict__ part, bf16* __restrict__ y,
-                                                                  long long MN, int S) {
-  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= MN) return;
-  float s = part[i];
-  for (int j = 1; j < S; ++j) s += part[(long long)j * MN + i];
-  y[i] = (bf16)s;
+// y = bf16(sum over splits of part[s]) in split order, for every projection of the launch; with
+// the SwiGLU epilogue (two projections of equal N) y0 = round(round(silu(gate)) * up) instead.
+__global__ __launch_bounds__(256) void decode_linear_reduce_kernel(LinArgs a, long long total) {
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total) return;
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < LIN_MAXSEG; ++i)
+    if (i < a.nseg && e >= a.seg[i].e0) si = i;
+  const long long MN0 = (long long)a.M * a.seg[si].N;
+  const long long i = e - a.seg[si].e0;
+  const float* p = a.seg[si].part + i;
+  float s = p[0];
+  for (int j = 1; j < a.S; ++j) s += p[(long long)j * MN0];
+  if (!a.swiglu) {
+    a.seg[si].y[i] = (bf16)s;
+    return;
+  }
+  const float* pu = a.seg[1].part + i;  // swiglu: index space is the gate's; up has the same shape
+  float su = pu[0];
+  for (int j = 1; j < a.S; ++j) su += pu[(long long)j * MN0];
+  const float g = round_through<bf16>(s), u = round_through<bf16>(su);
+  a.seg[0].y[i] = (bf16)(round_through<bf16>(silu_f32(g)) * u);
 }
 
 }  // namespace dllm
@@ -140,30 +181,58 @@ extern "C" int dllm_decode_linear_splits(int M, int N, int K) {
   return (int)s;
 }
 
-extern "C" int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, float* workspace, int M, int N, int K,
-                                      int splits, int dtype, void* stream) {
-  if (!x || !weight || !y) return fail(DLLM_EINVAL, "decode linear: null pointer");
-  if (M <= 0 || N <= 0 || K <= 0 || splits <= 0) return fail(DLLM_EINVAL, "decode linear: bad sizes M=%d N=%d K=%d", M, N, K);
+extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const void* const* weights,
+                                            void* const* outs, const int* Ns, float* workspace, int splits, int swiglu,
+                                            int dtype, void* stream) {
+  if (!x || !weights || !outs || !Ns) return fail(DLLM_EINVAL, "decode linear: null pointer");
+  if (count < 1 || count > LIN_MAXSEG) return fail(DLLM_EINVAL, "decode linear: %d projections (1..%d)", count, LIN_MAXSEG);
+  if (M <= 0 || K <= 0 || splits <= 0) return fail(DLLM_EINVAL, "decode linear: bad sizes M=%d K=%d", M, K);
   if (dtype != DT_BF16) return fail(DLLM_EUNSUPPORTED, "decode linear: bf16 only");
   if (K % 64) return fail(DLLM_EUNSUPPORTED, "decode linear: K=%d is not a multiple of 64", K);
   if (M > 64) return fail(DLLM_EUNSUPPORTED, "decode linear: M=%d > 64 rows (use a library GEMM)", M);
-  if (((uintptr_t)x | (uintptr_t)weight) & 15) return fail(DLLM_EINVAL, "decode linear: x and weight must be 16-byte aligned");
-  if (splits > 1 && !workspace) return fail(DLLM_EINVAL, "decode linear: %d splits need a workspace", splits);
-  // K range per split: a multiple of 64 (one staged step)
-  const int kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;
-  const int S = (K + kchunk - 1) / kchunk;
-  const long long tiles = (N + 127) / 128;
+  if ((uintptr_t)x & 15) return fail(DLLM_EINVAL, "decode linear: x must be 16-byte aligned");
+  if (swiglu && (count != 2 || Ns[0] != Ns[1])) return fail(DLLM_EINVAL, "decode linear: swiglu takes gate | up of equal N");
+  LinArgs a = {};
+  a.x = (const bf16*)x;
+  a.nseg = count;
+  a.M = M; a.K = K;
+  a.kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;  // K range per split: whole 64-k steps
+  a.S = (K + a.kchunk - 1) / a.kchunk;
+  a.swiglu = swiglu;
+  a.split_path = a.S > 1 || swiglu;
+  long long tiles = 0, elems = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!weights[i] || !outs[i] || Ns[i] <= 0) return fail(DLLM_EINVAL, "decode linear: projection %d is empty", i);
+    if ((uintptr_t)weights[i] & 15) return fail(DLLM_EINVAL, "decode linear: weights must be 16-byte aligned");
+    LinSeg& sg = a.seg[i];
+    sg.w = (const bf16*)weights[i];
+    sg.y = (bf16*)outs[i];
+    sg.N = Ns[i];
+    sg.tile0 = (int)tiles;
+    sg.e0 = elems;
+    sg.part = a.split_path ? workspace + (long long)a.S * elems : nullptr;
+    tiles += (Ns[i] + 127) / 128;
+    elems += (long long)M * Ns[i];
+  }
+  if (a.split_path && !workspace) return fail(DLLM_EINVAL, "decode linear: the split path needs a workspace");
   if (tiles > 0x7fffffffLL) return fail(DLLM_EUNSUPPORTED, "decode linear: grid too large");
   hipStream_t st = (hipStream_t)stream;
-  decode_linear_kernel<<<dim3((unsigned)tiles, S, (M + 31) / 32), 256, 0, st>>>(
-      (const bf16*)x, (const bf16*)weight, (bf16*)y, S > 1 ? workspace : nullptr, M, N, K, kchunk);
+  decode_linear_kernel<<<dim3((unsigned)tiles, a.S, (M + 31) / 32), 256, 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear launch: %s", hipGetErrorString(e));
-  if (S > 1) {
-    const long long MN = (long long)M * N;
-    decode_linear_reduce_kernel<<<dim3((unsigned)((MN + 255) / 256)), 256, 0, st>>>(workspace, (bf16*)y, MN, S);
+  if (a.split_path) {
+    const long long total = swiglu ? (long long)M * Ns[0] : elems;
+    decode_linear_reduce_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, st>>>(a, total);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear reduce launch: %s", hipGetErrorString(e));
   }
   return DLLM_OK;
+}
+
+extern "C" int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, float* workspace, int M, int N, int K,
+                                      int splits, int dtype, void* stream) {
+  const void* w[1] = {weight};
+  void* o[1] = {y};
+  const int n[1] = {N};
+  return dllm_decode_linear_multi_fwd(x, M, K, 1, w, o, n, workspace, splits, 0, dtype, stream);
 }

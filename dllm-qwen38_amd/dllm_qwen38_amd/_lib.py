@@ -21,6 +21,8 @@ _c_int = ctypes.c_int
 _c_float = ctypes.c_float
 _c_i64 = ctypes.c_int64
 _c_i64p = ctypes.POINTER(ctypes.c_int64)
+_c_voidpp = ctypes.POINTER(ctypes.c_void_p)
+_c_intp = ctypes.POINTER(ctypes.c_int)
 _c_fp = ctypes.c_void_p
 
 # name -> (restype, argtypes)
@@ -56,6 +58,8 @@ _SIGNATURES = {
     "dllm_decode_linear_splits": (_c_int, [_c_int, _c_int, _c_int]),
     "dllm_decode_linear_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_void_p]),
+    "dllm_decode_linear_multi_fwd": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_voidpp, _c_voidpp, _c_intp,
+                                              _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
     "dllm_block_causal_attention_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_void_p]),

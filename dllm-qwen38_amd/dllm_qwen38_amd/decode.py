@@ -19,6 +19,7 @@ Drop-in for the reference's `src/dllm_qwen38/decode.py`:
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass, field
 
 import torch
@@ -135,6 +136,58 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | 
     return y.reshape(*x.shape[:-1], N)
 
 
+def decode_linear_multi(x: torch.Tensor, weights: list, *, swiglu: bool = False):
+    """Up to four projections of the same x [..., K] in one launch (their weights [N_i, K] bf16).
+    Returns the list of [..., N_i] outputs, or with swiglu (gate, up) the MLP activation
+    round(round(silu(x gate^T)) * (x up^T)) as one tensor."""
+    dev = _lib.require_device(x, *weights)
+    K = x.shape[-1]
+    if not 1 <= len(weights) <= 4:
+        raise ValueError("decode_linear_multi takes 1 to 4 weights")
+    if any(w.dim() != 2 or w.shape[1] != K or w.dtype != torch.bfloat16 for w in weights) or x.dtype != torch.bfloat16:
+        raise ValueError(f"weights must be bf16 [N, {K}] and x bf16")
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    ws = [w.contiguous() for w in weights]
+    Ns = [w.shape[0] for w in ws]
+    if swiglu and (len(ws) != 2 or Ns[0] != Ns[1]):
+        raise ValueError("swiglu takes (gate, up) of equal N")
+    L = _lib.lib()
+    splits = L.dllm_decode_linear_splits(M, sum(-(-n // 128) * 128 for n in Ns), K)
+    if splits <= 0 or M > 64:
+        raise ValueError(f"decode_linear_multi does not take M={M} K={K} (M <= 64, K % 64 == 0)")
+    outs = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in (Ns[:1] if swiglu else Ns)]
+    if swiglu:
+        outs.append(outs[0])  # not written
+    work = (torch.empty(splits * M * sum(Ns), dtype=torch.float32, device=dev) if splits > 1 or swiglu else None)
+    n = len(ws)
+    warr = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
+    oarr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    narr = (ctypes.c_int * n)(*Ns)
+    _lib.check(L.dllm_decode_linear_multi_fwd(x2.data_ptr(), M, K, n, warr, oarr, narr, _lib.ptr(work), splits,
+                                              int(swiglu), _lib.dtype_code(x.dtype), _lib.stream_handle(dev)),
+               "dllm_decode_linear_multi_fwd")
+    lead = x.shape[:-1]
+    if swiglu:
+        return outs[0].reshape(*lead, Ns[0])
+    return [o.reshape(*lead, nn) for o, nn in zip(outs, Ns)]
+
+
+def _fast(lins, x: torch.Tensor) -> bool:
+    """Whether the decoding-step kernels take these projections of x (bf16 rows <= 64, no bias)."""
+    rows = x.numel() // x.shape[-1]
+    return (x.dtype == torch.bfloat16 and rows <= 64 and x.shape[-1] % 64 == 0
+            and all(lin.bias is None and lin.weight.dtype == torch.bfloat16 for lin in lins))
+
+
+def _proj_many(lins, x: torch.Tensor) -> list:
+    """Several projections of the same x: one launch on the decoding-step kernel, else one library
+    GEMM each."""
+    if _fast(lins, x):
+        return decode_linear_multi(x, [lin.weight for lin in lins])
+    return [lin(x) for lin in lins]
+
+
 def _proj(lin, x: torch.Tensor) -> torch.Tensor:
     """nn.Linear `lin` on x: the decoding-step kernel for a block of bf16 rows (at most 64), the
     library GEMM for the many rows of a prefill and for fp32 or biased projections."""
@@ -147,8 +200,13 @@ def _proj(lin, x: torch.Tensor) -> torch.Tensor:
 
 
 def _mlp(m, x: torch.Tensor) -> torch.Tensor:
-    """SwiGLU MLP ([hf]:704-717) with the decoding-step projections."""
-    return _proj(m.down_proj, norms.swiglu(_proj(m.gate_proj, x), _proj(m.up_proj, x)))
+    """SwiGLU MLP ([hf]:704-717): gate and up in one launch with the activation in its reduction,
+    then the down projection."""
+    if _fast((m.gate_proj, m.up_proj), x):
+        act = decode_linear_multi(x, [m.gate_proj.weight, m.up_proj.weight], swiglu=True)
+    else:
+        act = norms.swiglu(m.gate_proj(x), m.up_proj(x))
+    return _proj(m.down_proj, act)
 
 
 class PrefixCache:
@@ -205,9 +263,8 @@ def _gdn_segment(m, x: torch.Tensor, cache: PrefixCache, i: int, commit: bool) -
     prefix's last projections in, the recurrence starts from the prefix state; with commit, the
     state after the segment and its last projections replace the cached ones."""
     B, T, _ = x.shape
-    raw = _proj(m.in_proj_qkv, x)  # [B, T, conv_dim]
-    z = _proj(m.in_proj_z, x)
-    beta, g = gdn._beta_g(m, _proj(m.in_proj_b, x), _proj(m.in_proj_a, x))
+    raw, z, bp, ap = _proj_many((m.in_proj_qkv, m.in_proj_z, m.in_proj_b, m.in_proj_a), x)  # raw [B, T, conv_dim]
+    beta, g = gdn._beta_g(m, bp, ap)
     mixed = gdn.causal_conv1d_fn(raw.transpose(1, 2), m.conv1d.weight.squeeze(1), m.conv1d.bias,
                                  activation=m.activation, conv_prefix=cache.conv[i]).transpose(1, 2)
     q, k, v = gdn._split_qkv(mixed, m, B, T)
@@ -231,12 +288,13 @@ def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: i
     block-causal attention against cache rows 0..pos0+T-1, sigmoid gate, o_proj."""
     B, T, _ = x.shape
     hd = att.head_dim
-    q, gate = torch.chunk(_proj(att.q_proj, x).view(B, T, -1, 2 * hd), 2, dim=-1)
+    qg, kp, vp = _proj_many((att.q_proj, att.k_proj, att.v_proj), x)
+    q, gate = torch.chunk(qg.view(B, T, -1, 2 * hd), 2, dim=-1)
     gate = gate.reshape(B, T, -1)
     cos, sin = cache.cos[pos0:pos0 + T], cache.sin[pos0:pos0 + T]
-    q, k = norms.qk_norm_rope(q, _proj(att.k_proj, x).view(B, T, -1, hd), att.q_norm, att.k_norm, cos, sin, T)
+    q, k = norms.qk_norm_rope(q, kp.view(B, T, -1, hd), att.q_norm, att.k_norm, cos, sin, T)
     cache.k[i][:, pos0:pos0 + T] = k
-    cache.v[i][:, pos0:pos0 + T] = _proj(att.v_proj, x).view(B, T, -1, hd)
+    cache.v[i][:, pos0:pos0 + T] = vp.view(B, T, -1, hd)
     o = attention.block_causal_attention(q, cache.k[i][:, :pos0 + T], cache.v[i][:, :pos0 + T], block=cache.block,
                                          q_offset=pos0, scale=float(att.scaling))
     return _proj(att.o_proj, o.reshape(B, T, -1) * torch.sigmoid(gate))

@@ -153,6 +153,17 @@ int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, float* wo
                            int splits, int dtype, void* stream);
 
 /*
+ * Up to four projections of the same x in one launch (q | k | v; in_proj_qkv | z | b | a; gate |
+ * up): weights[i] [Ns[i], K] -> outs[i] [M, Ns[i]], one split count for all (splits from
+ * dllm_decode_linear_splits(M, sum of Ns rounded up to 128, K)). workspace holds
+ * splits * M * sum(Ns) floats when splits > 1 or swiglu. swiglu = 1 (two projections gate | up
+ * of equal N): outs[0] receives round(round(silu(gate)) * up), the MLP activation of
+ * [hf]:704-717, and outs[1] is not written.
+ */
+int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const void* const* weights, void* const* outs,
+                                 const int* Ns, float* workspace, int splits, int swiglu, int dtype, void* stream);
+
+/*
  * Qwen3.5 RMSNorm over the last dim of x [rows, dim]: y = x * rsqrt(mean(x^2) + eps) * (1 + w)
  * in fp32 (unit_offset = 1; 0 applies w as is), rounded once to x's dtype.
  * Replaces [hf]:720-737 Qwen3_5RMSNorm as called by the decoder layer and the final norm

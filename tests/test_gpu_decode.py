@@ -103,6 +103,30 @@ def test_decode_linear_matches_fp32_reference(dev, M, N, K):
     assert torch.equal(got, again), "split-K sums must be deterministic"
 
 
+def test_decode_linear_multi_and_swiglu_epilogue(dev):
+    """Projections sharing x in one launch equal the fp32 reference as single ones do; the SwiGLU
+    epilogue equals round(round(silu(g)) * u) of the rounded projections within two bf16 ulps."""
+    g = torch.Generator().manual_seed(77)
+    M, K = 32, 5120
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    ws = [(torch.randn(n, K, generator=g) * 0.02).to(torch.bfloat16) for n in (10240, 6144, 48, 48)]
+    outs = decode.decode_linear_multi(x.to(dev), [w.to(dev) for w in ws])
+    torch.cuda.synchronize()
+    for o, w in zip(outs, ws):
+        ref = x.float() @ w.float().T
+        err = (o.float().cpu() - ref).abs()
+        assert (err <= 2 ** -8 * ref.abs() + 2 ** -16 * (x.float().abs() @ w.float().abs().T)).all()
+    gw, uw = ((torch.randn(2048, K, generator=g) * 0.02).to(torch.bfloat16) for _ in range(2))
+    act = decode.decode_linear_multi(x.to(dev), [gw.to(dev), uw.to(dev)], swiglu=True)
+    torch.cuda.synchronize()
+    gr = (x.float() @ gw.float().T).to(torch.bfloat16).float()
+    ur = (x.float() @ uw.float().T).to(torch.bfloat16).float()
+    ref = (torch.nn.functional.silu(gr).to(torch.bfloat16).float() * ur)
+    err = (act.float().cpu() - ref).abs()
+    print(f"swiglu epilogue max|d|={err.max():.3e} max|ref|={ref.abs().max():.3e}")
+    assert (err <= 2 ** -6 * ref.abs() + 2 ** -10 * ref.abs().max()).all()
+
+
 @pytest.fixture(scope="module")
 def tiny(dev):
     cpu_model, cpu_head = tiny_hf_model(seed=0)

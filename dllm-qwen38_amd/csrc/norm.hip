@@ -103,6 +103,23 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict_
   }
 }
 
+// Gated DeltaNet gates of every (token, value head): beta = round_T(sigmoid(b)) held in fp32, and
+// g = -exp(A_log) * softplus(a + dt_bias) in fp32 (softplus linear above 20, as torch's).
+template <typename T, typename TP>
+__global__ __launch_bounds__(256) void gdn_gates_kernel(const T* __restrict__ b, const T* __restrict__ a,
+                                                        const TP* __restrict__ a_log, const TP* __restrict__ dt_bias,
+                                                        float* __restrict__ beta, float* __restrict__ g, long long n,
+                                                        int H) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int h = (int)(i % H);
+  const float bv = to_f32(b[i]);
+  beta[i] = round_through<T>(1.f / (1.f + expf(-bv)));
+  const float av = to_f32(a[i]) + to_f32(dt_bias[h]);
+  const float sp = av > 20.f ? av : log1pf(expf(av));
+  g[i] = -expf(to_f32(a_log[h])) * sp;
+}
+
 // out = round_T(round_T(silu(g)) * u)
 template <typename T>
 __global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ g, const T* __restrict__ u,
@@ -242,6 +259,27 @@ extern "C" int dllm_gated_rmsnorm_fwd(const void* x, const void* z, const void* 
     return fail(DLLM_EUNSUPPORTED, "gated rmsnorm: dtype pair (%d, %d) not supported", dtype, dtype_w);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "gated rmsnorm launch: %s", hipGetErrorString(e));
+}
+
+extern "C" int dllm_gdn_gates_fwd(const void* b, const void* a, const void* a_log, const void* dt_bias, float* beta,
+                                  float* g, int64_t rows, int heads, int dtype, int dtype_param, void* stream) {
+  if (!b || !a || !a_log || !dt_bias || !beta || !g) return fail(DLLM_EINVAL, "gdn gates: null pointer");
+  if (rows <= 0 || heads <= 0) return fail(DLLM_EINVAL, "gdn gates: bad sizes rows=%lld heads=%d", (long long)rows, heads);
+  const long long n = (long long)rows * heads;
+  const long long nb = (n + 255) / 256;
+  if (nb > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "gdn gates: too large");
+  hipStream_t st = (hipStream_t)stream;
+#define GATES(T, TP)                                                                                        \
+  gdn_gates_kernel<T, TP><<<dim3((unsigned)nb), dim3(256), 0, st>>>((const T*)b, (const T*)a, (const TP*)a_log, \
+                                                                   (const TP*)dt_bias, beta, g, n, heads)
+  if (dtype == DT_BF16 && dtype_param == DT_F32) GATES(bf16, float);
+  else if (dtype == DT_BF16 && dtype_param == DT_BF16) GATES(bf16, bf16);
+  else if (dtype == DT_F32 && dtype_param == DT_F32) GATES(float, float);
+  else if (dtype == DT_F32 && dtype_param == DT_BF16) GATES(float, bf16);
+  else return fail(DLLM_EUNSUPPORTED, "gdn gates: dtype pair (%d, %d) not supported", dtype, dtype_param);
+#undef GATES
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "gdn gates launch: %s", hipGetErrorString(e));
 }
 
 extern "C" int dllm_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {

@@ -15,9 +15,8 @@ q/k are never expanded.
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 
-from . import _lib
+from . import _lib, norms
 
 # Which core the last call used and why — reports name the path they measured (gdn.py:22-24).
 _IMPL = {"force": None, "last": "hip", "reason": ""}
@@ -133,11 +132,9 @@ def causal_conv1d_fn(hidden_states: torch.Tensor, weight: torch.Tensor, bias: to
 
 
 def _beta_g(m, b: torch.Tensor, a: torch.Tensor):
-    """beta = sigmoid(b) in the projection dtype; g = -exp(A_log) * softplus(a + dt_bias) in fp32
-    (reference gdn.py:225-226)."""
-    beta = b.sigmoid()
-    g = -m.A_log.float().exp() * F.softplus(a.float() + m.dt_bias)
-    return beta, g
+    """beta = sigmoid(b) rounded to the projection dtype (returned in fp32, as the core takes it);
+    g = -exp(A_log) * softplus(a + dt_bias) in fp32 (reference gdn.py:225-226); one HIP kernel."""
+    return norms.gdn_gates(b, a, m.A_log, m.dt_bias)
 
 
 def _split_qkv(mixed: torch.Tensor, m, B: int, T: int):

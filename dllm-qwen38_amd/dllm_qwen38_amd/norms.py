@@ -91,3 +91,24 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_norm, k_norm, cos: torch.Te
         cs.data_ptr(), sn.data_ptr(), qo.data_ptr(), ko.data_ptr(), B, S, L, Hq, Hkv, hd, rd, _eps(q_norm),
         _lib.dtype_code(q.dtype), _lib.dtype_code(wq.dtype), _lib.stream_handle(dev)), "dllm_qk_norm_rope_fwd")
     return qo, ko
+
+
+def gdn_gates(b: torch.Tensor, a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor):
+    """Gated DeltaNet gates (reference gdn.py:225-226) in one kernel: beta = sigmoid(b) rounded to
+    b's dtype and returned in fp32 (the core takes fp32 beta), g = -exp(A_log) * softplus(a + dt_bias)
+    in fp32. b, a [..., H] -> (beta, g) [..., H] fp32."""
+    dev = _lib.require_device(b, a, a_log, dt_bias)
+    H = b.shape[-1]
+    if a.shape != b.shape or a.dtype != b.dtype:
+        raise ValueError("b and a must share shape and dtype")
+    if a_log.numel() != H or dt_bias.numel() != H:
+        raise ValueError(f"A_log and dt_bias must have {H} entries")
+    p_dt = a_log.dtype
+    al, db = _c(a_log.reshape(H)), _c(dt_bias.reshape(H).to(p_dt))
+    bc, ac = _c(b), _c(a)
+    beta = torch.empty(b.shape, dtype=torch.float32, device=dev)
+    g = torch.empty(b.shape, dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().dllm_gdn_gates_fwd(bc.data_ptr(), ac.data_ptr(), al.data_ptr(), db.data_ptr(), beta.data_ptr(),
+                                             g.data_ptr(), b.numel() // H, H, _lib.dtype_code(b.dtype),
+                                             _lib.dtype_code(p_dt), _lib.stream_handle(dev)), "dllm_gdn_gates_fwd")
+    return beta, g

@@ -183,6 +183,15 @@ int dllm_gated_rmsnorm_fwd(const void* x, const void* z, const void* weight, voi
                            float eps, int dtype, int dtype_w, void* stream);
 
 /*
+ * Gated DeltaNet gates (src/dllm_qwen38/gdn.py:225-226): beta = sigmoid(b) rounded to the input
+ * dtype and held in fp32 (the core's beta), g = -exp(A_log) * softplus(a + dt_bias) in fp32
+ * (softplus linear above 20). b, a [rows, heads] contiguous in dtype; A_log, dt_bias [heads] in
+ * dtype_param; beta, g [rows, heads] fp32.
+ */
+int dllm_gdn_gates_fwd(const void* b, const void* a, const void* a_log, const void* dt_bias, float* beta, float* g,
+                       int64_t rows, int heads, int dtype, int dtype_param, void* stream);
+
+/*
  * SwiGLU product of the MLP: out = round(round(silu(gate)) * up), n elements, 16-byte aligned.
  * Replaces the act_fn(gate_proj(x)) * up_proj(x) of [hf]:704-717.
  */

@@ -86,3 +86,25 @@ def test_qk_norm_rope(dev, dtype, Hq, Hkv, hd, rd):
     k_ref = attn_ref.apply_rope(model_ref.rmsnorm(k, wk, 1e-6), c2, s2)
     _close(qo, q_ref, dtype, f"q {dtype} hd{hd} rd{rd}", floor=2 ** -8)
     _close(ko, k_ref, dtype, f"k {dtype} hd{hd} rd{rd}", floor=2 ** -8)
+
+
+@pytest.mark.parametrize("dtype,pdtype", [(torch.bfloat16, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                          (torch.float32, torch.float32)])
+def test_gdn_gates_match_torch(dev, dtype, pdtype):
+    """beta = sigmoid(b) rounded to b's dtype: within one ulp of bf16, or within 4 fp32 ulps (two
+    exp implementations and the reciprocal, each within a couple of ulps); g = -exp(A_log) *
+    softplus(a + dt_bias) in fp32 (relative 1e-6), including the linear branch of softplus above 20."""
+    g = torch.Generator().manual_seed(3)
+    H = 48
+    b = (torch.randn(7, 33, H, generator=g) * 4).to(dtype)
+    a = (torch.randn(7, 33, H, generator=g) * 12).to(dtype)
+    a_log = torch.log(torch.rand(H, generator=g) * 15 + 1).to(pdtype)
+    dt_bias = torch.randn(H, generator=g).to(pdtype)
+    beta, gg = norms.gdn_gates(b.to(dev), a.to(dev), a_log.to(dev), dt_bias.to(dev))
+    torch.cuda.synchronize()
+    rb = b.float().sigmoid().to(dtype).float()
+    ulp = (1 if dtype == torch.bfloat16 else 4) * torch.finfo(dtype).eps * rb.abs().clamp_min(torch.finfo(dtype).tiny)
+    assert ((beta.cpu() - rb).abs() <= ulp).all()
+    rg = -a_log.float().exp() * torch.nn.functional.softplus(a.float() + dt_bias.float())
+    assert ((gg.cpu() - rg).abs() <= 1e-6 * rg.abs() + 1e-30).all()
+    assert (a.float() + dt_bias.float() > 20).any()

@@ -50,13 +50,15 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x, c
       }
     }
     const float inv = rsqrtf(wave_sum(ss) / (float)dim + eps);
+    typedef __attribute__((ext_vector_type(8))) TW W8;  // weights as vectors too (16 or 32 bytes)
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c0 = (k * 64 + lane) * 8;
+      const W8 wv = *(const W8*)(w + c0);
       V8 yv;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float wf = to_f32(w[c0 + i]);
+        const float wf = to_f32(wv[i]);
         yv[i] = from_f32<T>(v[k][i] * inv * (unit ? 1.f + wf : wf));
       }
       *(V8*)(y + base + c0) = yv;
@@ -231,7 +233,7 @@ extern "C" int dllm_rmsnorm_fwd(const void* x, const void* residual, void* sum_o
   if (rows < 0 || dim <= 0) return fail(DLLM_EINVAL, "rmsnorm: bad sizes rows=%d dim=%d", rows, dim);
   if (sum_out && !residual) return fail(DLLM_EINVAL, "rmsnorm: sum_out needs a residual");
   if (rows == 0) return DLLM_OK;
-  const bool vec = ((uintptr_t)x | (uintptr_t)y | (uintptr_t)residual | (uintptr_t)sum_out) % 16 == 0;
+  const bool vec = ((uintptr_t)x | (uintptr_t)y | (uintptr_t)residual | (uintptr_t)sum_out | (uintptr_t)weight) % 16 == 0;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DT_BF16 && dtype_w == DT_BF16)
     return launch_rmsnorm<bf16, bf16>(x, residual, sum_out, weight, y, rows, dim, eps, unit_offset, vec, st);

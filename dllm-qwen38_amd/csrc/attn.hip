@@ -42,6 +42,9 @@ struct AttnArgs {
   int B, L, Hq, Hkv, d, C;
   int leak;
   int M, N, q0;       // block-causal mode: query rows, key rows, absolute position of query row 0
+  int ksplit;         // block-causal mode, direct-load kernel: key tiles split over grid.y
+  float* opart;       // ksplit > 1: unnormalised O [ksplit][B][M][Hq][d] fp32
+  float* mlpart;      // ksplit > 1: running max and sum [ksplit][B][M][Hq][2] fp32
   float scale_log2e;  // softmax scale * log2(e)
   int vec;            // 16-byte vector loads of q/k/v rows allowed
 };
@@ -481,6 +484,16 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
     if (n < n1) { kh = 1; j0 = (t1lo + n) * 32; }
     else { kh = 0; j0 = (t0lo + n - n1) * 32; }
   };
+  // key tiles of this workgroup: all of them, or (block-causal with a key split) one contiguous
+  // share; the shares' partial results are merged by attn_combine_kernel
+  int nbeg = 0, nend = ntiles;
+  if constexpr (BC) {
+    if (a.ksplit > 1) {
+      const int per = (ntiles + a.ksplit - 1) / a.ksplit;
+      nbeg = min(ntiles, (int)blockIdx.y * per);
+      nend = min(ntiles, nbeg + per);
+    }
+  }
 
   const bf16* const qbase = (const bf16*)a.q + b * a.q_sb + (long long)hq * a.q_sh;
   const bf16* const kbase = (const bf16*)a.k + b * a.k_sb + (long long)hkv * a.k_sh;
@@ -523,7 +536,7 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   };
   // wait until tile n's loads (this wave's) have landed, given which later tiles were issued
   auto wait_tile = [&](int n) {
-    const int ahead = min(NST - 2, ntiles - 1 - n);  // tiles issued after n and still allowed in flight
+    const int ahead = min(NST - 2, nend - 1 - n);  // tiles issued after n and still allowed in flight
     if (ahead >= 2) wait_vmcnt<2 * IPW>();
     else if (ahead == 1) wait_vmcnt<IPW>();
     else wait_vmcnt<0>();
@@ -537,11 +550,11 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
 
 #pragma unroll
   for (int n = 0; n < NST - 1; ++n)
-    if (n < ntiles) stage_tile(n);
-  if (ntiles > 0) wait_tile(0);
+    if (nbeg + n < nend) stage_tile(nbeg + n);
+  if (nend > nbeg) wait_tile(nbeg);
   __syncthreads();
-  for (int n = 0; n < ntiles; ++n) {
-    if (n + NST - 1 < ntiles) stage_tile(n + NST - 1);  // its stage held tile n - 1, done before the barrier
+  for (int n = nbeg; n < nend; ++n) {
+    if (n + NST - 1 < nend) stage_tile(n + NST - 1);  // its stage held tile n - 1, done before the barrier
     int kh, j0;
     tile_pos(n, kh, j0);
     const int kb0 = j0 / C, kb1 = (min(Lk, j0 + 32) - 1) / C;
@@ -616,11 +629,33 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
         mma32(O[t], vf, pf);
       }
     }
-    if (n + 1 < ntiles) wait_tile(n + 1);
+    if (n + 1 < nend) wait_tile(n + 1);
     __syncthreads();  // tile n + 1 staged by every wave; every wave is done with tile n's stage
   }
 
   const int qi = r0 + l32;
+  if constexpr (BC) {
+    if (a.ksplit > 1) {  // partial result of this key share, unnormalised
+      if (wave_live && qi < Lq) {
+        const long long prow = (((long long)blockIdx.y * a.B + b) * Lq + qi) * a.Hq + hq;
+        float* op = a.opart + prow * D + e * DH;
+#pragma unroll
+        for (int t = 0; t < SH; ++t)
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            f32x4 o4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o4[i] = O[t][4 * m + i];
+            *(f32x4*)(op + 32 * t + 8 * m + 4 * h) = o4;
+          }
+        if (e == 0 && h == 0) {
+          a.mlpart[2 * prow] = mrow;
+          a.mlpart[2 * prow + 1] = lrow;
+        }
+      }
+      return;
+    }
+  }
   if (wave_live && qi < Lq) {
     const float inv = 1.f / lrow;
     const long long orow = BC ? (long long)b * Lq + qi : (long long)b * 2 * L + qh * L + qi;
@@ -637,15 +672,53 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   }
 }
 
+// Merge of the key shares of a split block-causal launch: per (b, query, head) row, with
+// M = max_s m_s and w_s = 2^(m_s - M), out = (sum_s w_s O_s) / (sum_s w_s l_s). One thread per
+// four consecutive d.
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ opart,
+                                                           const float* __restrict__ mlpart, bf16* __restrict__ out,
+                                                           long long rows, int d, int ks) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int q4 = d / 4;
+  if (t >= rows * q4) return;
+  const long long row = t / q4;
+  const int c = (int)(t % q4) * 4;
+  float mx = -1e30f;
+  for (int s = 0; s < ks; ++s) mx = fmaxf(mx, mlpart[2 * (s * rows + row)]);
+  float l = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < ks; ++s) {
+    const float w = __builtin_amdgcn_exp2f(mlpart[2 * (s * rows + row)] - mx);
+    l += w * mlpart[2 * (s * rows + row) + 1];
+    const f32x4 p = *(const f32x4*)(opart + (s * rows + row) * d + c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] += w * p[i];
+  }
+  const float inv = 1.f / l;
+  bf16x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = (bf16)(o[i] * inv);
+  *(bf16x4*)(out + row * d + c) = r;
+}
+
 template <int D, bool BC>
 static int launch_attn_dma(const AttnArgs& a, hipStream_t st) {
   const int ntq = ((BC ? a.M : a.L) + 31) / 32;
   const int ng = (ntq + 3) / 4;
   const long long nblk = (long long)ng * (BC ? 1 : 2) * a.B * a.Hq;
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "attention: grid too large");
-  bd_attn_dma_kernel<D, BC><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  const int ks = BC && a.ksplit > 1 ? a.ksplit : 1;
+  bd_attn_dma_kernel<D, BC><<<dim3((unsigned)nblk, ks), dim3(512), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention launch: %s", hipGetErrorString(e));
+  if (ks > 1) {
+    const long long rows = (long long)a.B * a.M * a.Hq;
+    const long long n = rows * (D / 4);
+    attn_combine_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a.opart, a.mlpart, (bf16*)a.out,
+                                                                                rows, D, ks);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention combine launch: %s", hipGetErrorString(e));
+  }
   return DLLM_OK;
 }
 
@@ -727,13 +800,16 @@ extern "C" int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, co
 extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, const void* k,
                                                const int64_t* k_strides, const void* v, const int64_t* v_strides,
                                                void* out, int B, int M, int N, int q0, int Hq, int Hkv, int d,
-                                               int block, float scale, int dtype, void* stream) {
+                                               int block, float scale, int dtype, float* workspace, int key_splits,
+                                               void* stream) {
   if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides)
     return fail(DLLM_EINVAL, "block-causal attention: null pointer");
   if (B <= 0 || M <= 0 || N <= 0 || q0 < 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || block <= 0)
     return fail(DLLM_EINVAL, "block-causal attention: bad sizes B=%d M=%d N=%d q0=%d Hq=%d Hkv=%d d=%d block=%d", B,
                 M, N, q0, Hq, Hkv, d, block);
   if ((long long)q0 + M > 0x7fffffffLL) return fail(DLLM_EINVAL, "block-causal attention: q0 + M overflows");
+  if (key_splits < 1 || key_splits > 64) return fail(DLLM_EINVAL, "block-causal attention: key_splits=%d (1..64)", key_splits);
+  if (key_splits > 1 && !workspace) return fail(DLLM_EINVAL, "block-causal attention: key splits need a workspace");
   if (Hq % Hkv) return fail(DLLM_EINVAL, "attention: Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
   if (d > 256) return fail(DLLM_EUNSUPPORTED, "attention: head_dim %d > 256 not supported", d);
   const int64_t* const sts[3] = {q_strides, k_strides, v_strides};
@@ -748,6 +824,9 @@ extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_s
   fill_strides(a, q_strides, k_strides, v_strides);
   a.B = B; a.L = 0; a.Hq = Hq; a.Hkv = Hkv; a.d = d; a.C = block;
   a.M = M; a.N = N; a.q0 = q0;
+  a.ksplit = key_splits;
+  a.opart = workspace;
+  a.mlpart = workspace ? workspace + (long long)key_splits * B * M * Hq * d : nullptr;
   a.scale_log2e = scale * 1.4426950408889634f;
   return dispatch_attn<true>(a, sts, dtype, (hipStream_t)stream);
 }

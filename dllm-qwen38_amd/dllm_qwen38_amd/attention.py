@@ -74,15 +74,25 @@ def bd_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: in
     return out
 
 
+def _key_splits(q: torch.Tensor, M: int, N: int, d: int) -> int:
+    """Key splits for a decoding step (bf16, the direct-load kernel's head sizes, few query rows):
+    about eight 32-key tiles per workgroup; 1 otherwise."""
+    if q.dtype != torch.bfloat16 or d not in (64, 128, 256) or M > 64 or N < 512:
+        return 1
+    return max(1, min(32, -(-N // 256)))
+
+
 def block_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int, q_offset: int = 0,
-                           scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                           scale: float | None = None, out: torch.Tensor | None = None,
+                           key_splits: int | None = None) -> torch.Tensor:
     """Block-causal attention of a query segment against a key/value cache (the clean-prefix cache
     of the cached decoder; the reference re-runs the whole forward instead, decode.py:63-66).
 
     q [B, M, Hq, d] at absolute positions q_offset..q_offset+M-1; k/v [B, N, Hkv, d] at positions
     0..N-1 (token-major, any batch/token/head strides, last dim contiguous; rotary already applied).
     Query i sees key j iff j // block <= (q_offset + i) // block (blockdiff.py:43-47 with the query
-    rows offset). Returns [B, M, Hq, d]."""
+    rows offset). Returns [B, M, Hq, d]. key_splits (default: chosen for a decoding step's few query
+    rows) spreads the key tiles over several workgroups whose partial results are merged."""
     dev = _lib.require_device(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q must be [B, M, Hq, d] and k, v [B, N, Hkv, d]")
@@ -102,10 +112,12 @@ def block_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     elif tuple(out.shape) != (B, M, Hq, d) or not out.is_contiguous() or out.dtype != q.dtype:
         raise ValueError("out must be a contiguous [B, M, Hq, d] tensor of q's dtype")
     sc = d ** -0.5 if scale is None else float(scale)
+    ks = _key_splits(q, M, N, d) if key_splits is None else int(key_splits)
+    work = torch.empty(ks * B * M * Hq * (d + 2), dtype=torch.float32, device=dev) if ks > 1 else None
     _lib.check(_lib.lib().dllm_block_causal_attention_fwd(
         q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
-        out.data_ptr(), B, M, N, q_offset, Hq, Hkv, d, block, sc, _lib.dtype_code(q.dtype), _lib.stream_handle(dev)),
-        "dllm_block_causal_attention_fwd")
+        out.data_ptr(), B, M, N, q_offset, Hq, Hkv, d, block, sc, _lib.dtype_code(q.dtype), _lib.ptr(work), ks,
+        _lib.stream_handle(dev)), "dllm_block_causal_attention_fwd")
     return out
 
 

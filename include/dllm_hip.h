@@ -133,10 +133,15 @@ int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, const void* k
  * key j iff j/block <= (q0+i)/block. A denoising step is M = block, q0 = N - block (every key
  * visible); a prompt prefill is q0 = 0, M = N. Strides {b,t,h} in elements, last dim contiguous;
  * out [B,M,Hq,d] contiguous, same dtype. Same numerics as dllm_bd_attention_fwd; d <= 256.
+ * key_splits > 1 (bf16, d in {64,128,256}; a decoding step's few query rows against a long cache):
+ * the key tiles are split over that many workgroups per query tile and head, and a second launch
+ * merges their partial results (flash-decoding); workspace then holds key_splits*B*M*Hq*(d+2)
+ * floats. Other shapes ignore key_splits.
  */
 int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                                     const void* v, const int64_t* v_strides, void* out, int B, int M, int N, int q0,
-                                    int Hq, int Hkv, int d, int block, float scale, int dtype, void* stream);
+                                    int Hq, int Hkv, int d, int block, float scale, int dtype, float* workspace,
+                                    int key_splits, void* stream);
 
 /*
  * Projections of a decoding step (few token rows): y[M,N] = x[M,K] W[N,K]^T, bf16 in and out, fp32

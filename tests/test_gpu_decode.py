@@ -74,6 +74,20 @@ def test_prefill_is_bit_equal_to_the_clean_half_of_the_two_stream_kernel(dev, dt
     assert torch.equal(clean, both[:, L:])
 
 
+@pytest.mark.parametrize("ks", [2, 5, 16, 32])
+def test_key_split_attention_matches_oracle(dev, ks):
+    """Key tiles split over workgroups and merged (flash-decoding), including more splits than key
+    tiles (empty shares): within the bf16 bar of the oracle, as the unsplit kernel."""
+    q, k, v = _att_inputs(2, 32, 600, 8, 2, 256, torch.bfloat16, seed=ks)
+    got = attention.block_causal_attention(q.to(dev), k.to(dev), v.to(dev), block=32, q_offset=568, key_splits=ks)
+    one = attention.block_causal_attention(q.to(dev), k.to(dev), v.to(dev), block=32, q_offset=568, key_splits=1)
+    torch.cuda.synchronize()
+    ref = attn_ref.block_causal_attention(q, k, v, block=32, q_offset=568)
+    vmax = v.float().abs().max().item()
+    _check_att(got, ref, torch.bfloat16, vmax, f"key splits {ks}")
+    _check_att(one, ref, torch.bfloat16, vmax, "unsplit")
+
+
 def test_27b_class_decoding_step_attention(dev):
     """24 query / 4 key-value heads of dim 256, 4096 cached keys, one block of 32 queries."""
     q, k, v = _att_inputs(1, 32, 4096, 24, 4, 256, torch.bfloat16, seed=27)

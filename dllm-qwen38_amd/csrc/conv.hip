@@ -45,6 +45,7 @@ __global__ __launch_bounds__(256) void conv_fork_kernel(
   const long long row_base = (long long)b * L * Cd;
   // clean prefix: raw0 positions kblk*block-(K-1)+j, zero before the sequence start
   float h0[K - 1][VEC], ht[K - 1][VEC];
+  TX tl[VEC * (K - 1)];  // this thread's conv tails, channel-major: VEC*(K-1) consecutive elements
 #pragma unroll
   for (int j = 0; j < K - 1; ++j) {
     const int p = fork_prefix_pos(kblk, j, block, K);
@@ -56,15 +57,29 @@ __global__ __launch_bounds__(256) void conv_fork_kernel(
 #pragma unroll
       for (int e = 0; e < VEC; ++e) xs[e] = src[e];
     }
-    if (tails) {
-      TX* dst = tails + ((long long)fork_row(b, kblk, nb) * Cd + c0) * (K - 1) + j;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) dst[(long long)e * (K - 1)] = xs[e];
-    }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
+      tl[e * (K - 1) + j] = xs[e];
       h0[j][e] = round_through<TW>(to_f32(xs[e]));
       ht[j][e] = cold_noised ? 0.f : h0[j][e];
+    }
+  }
+  if (tails) {
+    TX* dst = tails + ((long long)fork_row(b, kblk, nb) * Cd + c0) * (K - 1);
+    constexpr int TN = VEC * (K - 1);
+    constexpr int EPV16 = 16 / (int)sizeof(TX);
+    if constexpr (TN % EPV16 == 0) {  // whole 16-byte stores (aligned: c0 is a multiple of VEC)
+      typedef VecN<TX, EPV16> V16t;
+#pragma unroll
+      for (int i = 0; i < TN / EPV16; ++i) {
+        V16t v;
+#pragma unroll
+        for (int e = 0; e < EPV16; ++e) v.v[e] = tl[i * EPV16 + e];
+        *(V16t*)(dst + i * EPV16) = v;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TN; ++i) dst[i] = tl[i];
     }
   }
 
@@ -152,7 +167,8 @@ static int launch_fork(const void* raw0, const void* rawt, const void* w, const 
   const int nb = L / block;
   constexpr int V = 16 / sizeof(TX);  // 16-byte row segments per thread
   const bool vec_ok = (Cd % V == 0) && ((uintptr_t)raw0 % 16 == 0) && ((uintptr_t)rawt % 16 == 0) &&
-                      ((uintptr_t)y0 % 16 == 0) && ((uintptr_t)yt % 16 == 0);
+                      ((uintptr_t)y0 % 16 == 0) && ((uintptr_t)yt % 16 == 0) &&
+                      ((uintptr_t)tails % 16 == 0);  // tails rows of VEC*(K-1) elements are 16-byte multiples
   if (K == 4 && vec_ok) {
     const int groups = Cd / V;
     dim3 grid((groups + 255) / 256, nb, B);

@@ -717,6 +717,532 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
   }
 }
 
+// ============================================================================================
+// Pipelined state fork (bf16, Dk = Dv = 128, one workgroup per (sequence, value head)).
+//
+// The recurrence S <- e^gamma_last S + K^T (U - W S) is the only sequential dependency of a tile;
+// the Gram products, the inverse T = (I + A)^-1, W = T1 K and P = mask(Q K^T) depend on the tile's
+// inputs alone. Here they are formed one tile AHEAD, beside the state work of the current tile:
+//   waves 0-3 (state waves) each own 32 value columns of BOTH streams. They hold the clean state of
+//            their columns in MFMA accumulators and, per tile, compute the noised outputs from it
+//            (the clean state before the tile: the fork), then the clean outputs and the update.
+//   waves 4-7 (prep waves) load every input and prepare the next tile: wave 4 / 6 (clean / noised)
+//            K K^T, the decay/beta mask A, T by blocked forward substitution in fp32, W and the T2
+//            operand; wave 5 / 7 P with the q norms and decay folded in.
+// One tile = two barriers: a load phase (prep waves store the next tile's raw q/k and this tile's
+// v rows into LDS) and a compute phase (state(c) on waves 0-3 beside prep(c+1) on waves 4-7), with
+// every operand the two exchange double-buffered by tile parity. Each SIMD runs one state wave and
+// one prep wave. The arithmetic of every product and scaling is that of gdn_chunk_kernel, operand
+// for operand; W and P are produced as transposed MFMA products so that their LDS rows are written
+// four elements at a time.
+struct PipeSmem {
+  static constexpr int DK = 128;
+  static constexpr int QROW = DK + 8;          // bf16 row stride of q, k, W and v rows
+  static constexpr int TROW = 36;              // bf16 row stride of P
+  static constexpr int FROW = 36;              // fp32 [32][32] scratch row stride
+  static constexpr int ROWS = 32 * QROW * 2;   // one [32][QROW] bf16 buffer
+  static constexpr int PB = 32 * TROW * 2;
+  static constexpr int T2B = 64 * 16 * 2;      // T2 operand fragment, lane-major
+  static constexpr int VSB = 4 * 32 * 4;       // state-phase vectors: EGQ, RNK, EGLK, EG
+  static constexpr int VAB = 6 * 32 * 4;       // prep vectors: GAML, BET, EG, EGL, RNK, RNQ
+  static constexpr int FB = 32 * FROW * 4;
+  static constexpr int YB = 16 * 20 * 4;
+  // row buffers: Q[stream][parity], W[stream][parity], K clean [parity] + K noised (read only by
+  // the preparation, which finishes before the next load phase), V[stream]
+  static constexpr int O_Q = 0;
+  static constexpr int O_W = O_Q + 4 * ROWS;
+  static constexpr int O_K = O_W + 4 * ROWS;
+  static constexpr int O_V = O_K + 3 * ROWS;
+  static constexpr int O_P = O_V + 2 * ROWS;
+  static constexpr int O_T2 = O_P + 4 * PB;
+  static constexpr int O_VS = O_T2 + 4 * T2B;
+  static constexpr int O_VA = O_VS + 4 * VSB;
+  static constexpr int O_AF = O_VA + 2 * VAB;
+  static constexpr int O_TF = O_AF + 2 * FB;
+  static constexpr int O_YF = O_TF + 2 * FB;
+  static constexpr int TOTAL = O_YF + 2 * YB;
+  static_assert(TOTAL <= 160 * 1024, "LDS budget");
+};
+// vector slots (floats) inside the VS and VA blocks
+enum { VS_EGQ = 0, VS_RNK = 32, VS_EGLK = 64, VS_EG = 96 };
+enum { VA_GAML = 0, VA_BET = 32, VA_EG = 64, VA_EGL = 96, VA_RNK = 128, VA_RNQ = 160 };
+
+__global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
+  using SM = PipeSmem;
+  using F = Frag<true>;
+  constexpr int KT = 4;
+  constexpr int QROW = SM::QROW, TROW = SM::TROW, FROW = SM::FROW;
+  constexpr float LOG2E = 1.4426950408889634f;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const bool prep = wave >= 4;
+  const int u = wave & 3;            // state waves: column slice; prep waves: role
+  const int gs = u >> 1;             // prep waves: stream prepared (0 clean, 1 noised)
+  const bool isG = prep && (u & 1) == 0;
+
+  const int lin = xcd_linear_id(blockIdx.x, gridDim.x);
+  const int hv = lin % a.Hv;
+  const int b = lin / a.Hv;
+  const int hk = hv / (a.Hv / a.Hk);
+  const int ntiles = a.T / a.sub;
+
+  auto QB = [&](int s, int p) { return (bf16*)(smem + SM::O_Q + (2 * s + p) * SM::ROWS); };
+  auto WB = [&](int s, int p) { return (bf16*)(smem + SM::O_W + (2 * s + p) * SM::ROWS); };
+  auto KB = [&](int s, int p) { return (bf16*)(smem + SM::O_K + (s == 0 ? p : 2) * SM::ROWS); };
+  auto VB = [&](int s) { return (bf16*)(smem + SM::O_V + s * SM::ROWS); };
+  auto PBf = [&](int s, int p) { return (bf16*)(smem + SM::O_P + (2 * s + p) * SM::PB); };
+  auto T2f = [&](int s, int p) { return (bf16x8*)(smem + SM::O_T2 + (2 * s + p) * SM::T2B); };
+  auto VS = [&](int s, int p) { return (float*)(smem + SM::O_VS + (2 * s + p) * SM::VSB); };
+  auto VA = [&](int s) { return (float*)(smem + SM::O_VA + s * SM::VAB); };
+  auto AFf = [&](int s) { return (float*)(smem + SM::O_AF + s * SM::FB); };
+  auto TFf = [&](int s) { return (float*)(smem + SM::O_TF + s * SM::FB); };
+  auto YFf = [&](int s) { return (float*)(smem + SM::O_YF + s * SM::YB); };
+
+  // ---- prep waves: loads. Thread (row lr, segment lseg) of the 256 prep threads holds, for both
+  // streams, q and k columns [8 lseg, +8) and [64 + 8 lseg, +8) of tile row lr, and v likewise.
+  const int gt = tid & 255;
+  const int lr = gt >> 3, lseg = gt & 7;
+  const bool lreal = lr < a.sub;  // rows >= sub are zero padding (loaded from row 0, zeroed on use)
+  const int e0 = lseg * 8, e1 = 64 + lseg * 8;
+  bf16x8 rq[2][2], rk[2][2], rv[2][2];
+  float rg = 0.f, rb = 0.f;
+  auto issue_loads = [&](int tq, int tvv) {  // q/k (and g, beta) of tile tq, v of tile tvv; -1 = none
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const GdnStream& st = a.s[s];
+      if (tq >= 0) {
+        const int tok = tq * a.sub + (lreal ? lr : 0);
+        const bf16* qr = (const bf16*)st.q + b * a.q_sb + (long long)hk * a.q_sh + tok * a.q_st;
+        const bf16* kr = (const bf16*)st.k + b * a.k_sb + (long long)hk * a.k_sh + tok * a.k_st;
+        rq[s][0] = *(const bf16x8*)(qr + e0);
+        rq[s][1] = *(const bf16x8*)(qr + e1);
+        rk[s][0] = *(const bf16x8*)(kr + e0);
+        rk[s][1] = *(const bf16x8*)(kr + e1);
+      }
+      if (tvv >= 0) {
+        const int tok = tvv * a.sub + (lreal ? lr : 0);
+        const bf16* vr = (const bf16*)st.v + b * a.v_sb + (long long)hv * a.v_sh + tok * a.v_st;
+        rv[s][0] = *(const bf16x8*)(vr + e0);
+        rv[s][1] = *(const bf16x8*)(vr + e1);
+      }
+    }
+    // g and beta: every lane loads (padding rows from the last real row, zeroed on use), so that
+    // no constant is ever written to these registers while a load into them may be in flight
+    // (such a write makes the compiler wait for every outstanding load right after the issue)
+    if (isG && tq >= 0) {
+      const GdnStream& st = a.s[gs];
+      const int row = tq * a.sub + min(l32, a.sub - 1);
+      rg = st.g[b * a.g_sb + (long long)hv * a.g_sh + row * a.g_st];
+      rb = st.beta[b * a.b_sb + (long long)hv * a.b_sh + row * a.b_st];
+    }
+  };
+
+  // The two roles run separate loops with the same barrier sequence (two per tile), so that
+  // neither role's registers (prefetched inputs, the state) are held live through the other.
+  const bf16x8 vzero = {};
+  if (prep) {
+  issue_loads(0, -1);
+  for (int c = -1; c < ntiles; ++c) {
+    const int lo = opaque_v(l32), ho = opaque_v(h);  // lane indices for masks (see opaque_v)
+    __syncthreads();  // tile c-1's state phase and tile c's preparation are done
+    // ------------------------------------------------------------ load phase
+    {
+      const int pn = (c + 1) & 1;
+      if (c + 1 < ntiles) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          bf16x8 xq[2], xk[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            xq[i] = lreal ? rq[s][i] : vzero;
+            xk[i] = lreal ? rk[s][i] : vzero;
+          }
+          bf16* q = QB(s, pn) + lr * QROW;
+          bf16* k = KB(s, pn) + lr * QROW;
+          *(bf16x8*)(q + e0) = xq[0];
+          *(bf16x8*)(q + e1) = xq[1];
+          *(bf16x8*)(k + e0) = xk[0];
+          *(bf16x8*)(k + e1) = xk[1];
+          // q and k row norms: fp32 sums of squares over the row's 8 threads (DPP)
+          float ss = 0.f, sk = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float x = to_f32(xq[i >> 3][i & 7]);
+            const float y = to_f32(xk[i >> 3][i & 7]);
+            ss = __builtin_fmaf(x, x, ss);
+            sk = __builtin_fmaf(y, y, sk);
+          }
+          ss = dpp_sum8(ss);
+          sk = dpp_sum8(sk);
+          if (lseg == 0) {
+            VA(s)[VA_RNQ + lr] = a.l2norm ? a.scale * rsqrtf(ss + 1e-6f) : a.scale;
+            VA(s)[VA_RNK + lr] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
+          }
+        }
+        // cumulative decay of the next tile: inclusive scan of g over its rows (lanes 0..31)
+        if (isG) {
+          const bool greal = h == 0 && l32 < a.sub;
+          float x = greal ? rg : 0.f;
+          x += dpp_mov<0x111>(x);  // row_shr:1
+          x += dpp_mov<0x112>(x);  // row_shr:2
+          x += dpp_mov<0x114>(x);  // row_shr:4
+          x += dpp_mov<0x118>(x);  // row_shr:8
+          x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
+          const float gam = x;
+          const float gall = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 31));
+          if (h == 0) {
+            float* va = VA(gs);
+            va[VA_GAML + l32] = gam * LOG2E;
+            va[VA_BET + l32] = greal ? rb : 0.f;
+            va[VA_EG + l32] = __builtin_amdgcn_exp2f(gam * LOG2E);
+            va[VA_EGL + l32] = __builtin_amdgcn_exp2f((gall - gam) * LOG2E);
+          }
+        }
+      }
+      if (c >= 0) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          bf16* v = VB(s) + lr * QROW;
+          *(bf16x8*)(v + e0) = lreal ? rv[s][0] : vzero;
+          *(bf16x8*)(v + e1) = lreal ? rv[s][1] : vzero;
+        }
+      }
+    }
+    __syncthreads();
+    issue_loads(c + 2 < ntiles ? c + 2 : -1, c + 1 < ntiles ? c + 1 : -1);
+
+    // ------------------------------------------------------------ preparation of tile c + 1
+    {
+      if (c + 1 < ntiles) {
+        const int pn = (c + 1) & 1;
+        const float* va = VA(gs);
+        float* const vs = VS(gs, pn);
+        const bf16* const K = KB(gs, pn);
+        f32x4 gam4[4];
+        if (isG) {
+          // A = mask(beta_i k^_i . k^_j e^(gamma_i - gamma_j)), j < i, from the Gram K K^T
+          float* const AF = AFf(gs);
+          float* const TF = TFf(gs);
+          float* const YF = YFf(gs);
+          f32x16 acc = zero16();
+          F fa[KT];
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) lds_frag(K + l32 * QROW + kt * 32, h, fa[kt]);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(va + VA_GAML + 8 * m + 4 * h);
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fa[kt]);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2 * KT + 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2 * KT, 0);
+          const float gj = va[VA_GAML + l32];
+          f32x4 bet4[4], rnk4[4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            bet4[m] = *(const f32x4*)(va + VA_BET + 8 * m + 4 * h);
+            rnk4[m] = *(const f32x4*)(va + VA_RNK + 8 * m + 4 * h);
+          }
+          const float rj = va[VA_RNK + l32];
+          const float eglj = va[VA_EGL + l32];
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int i = 8 * m + 4 * h + e;
+              const float val = (bet4[m][e] * rnk4[m][e] * rj) * acc[4 * m + e] *
+                                __builtin_amdgcn_exp2f(gam4[m][e] - gj);
+              AF[i * FROW + l32] = (lo < 8 * m + 4 * ho + e) ? val : 0.f;
+            }
+          if (h == 0) {
+            vs[VS_EGLK + l32] = eglj * rj;
+            vs[VS_RNK + l32] = rj;
+            vs[VS_EG + l32] = va[VA_EG + l32];
+          }
+          wave_lds_sync();
+          // level 0: four 8x8 diagonal blocks, one column per lane (lanes 0..31); lanes of odd
+          // blocks also clear the block above (read as zero by level 2)
+          if (h == 0) {
+            const int bb = l32 >> 3, cc = lo & 7, o = 8 * bb;
+            f32x4 ar[8][2];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) {
+              ar[i][0] = *(const f32x4*)(AF + (o + i) * FROW + o);
+              ar[i][1] = *(const f32x4*)(AF + (o + i) * FROW + o + 4);
+            }
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+            for (int i = 1; i < 8; ++i) {
+              float sacc = 0.f;
+#pragma unroll
+              for (int j = 0; j < i; ++j) sacc = __builtin_fmaf(ar[i][j >> 2][j & 3], x[j], sacc);
+              if (i > cc) x[i] = -sacc;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) TF[(o + i) * FROW + o + cc] = x[i];
+            if (bb & 1) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) TF[(o - 8 + i) * FROW + o + cc] = 0.f;
+            }
+          }
+          wave_lds_sync();
+          // level 1: T[m+1][m] = -D[m+1] (A[m+1][m] D[m]) for the three sub-diagonal 8x8 blocks
+          {
+            const int ii = lane >> 3, jj = lane & 7;
+            f32x4 arow[3][2];
+            float dcol[3][8];
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              arow[m][0] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m);
+              arow[m][1] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m + 4);
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) dcol[m][kk] = TF[(8 * m + kk) * FROW + 8 * m + jj];
+            }
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              float sacc = 0.f;
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(arow[m][kk >> 2][kk & 3], dcol[m][kk], sacc);
+              YF[m * 64 + ii * 8 + jj] = sacc;
+            }
+            wave_lds_sync();
+            f32x4 drow[3][2];
+            float ycol[3][8];
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              drow[m][0] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1));
+              drow[m][1] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1) + 4);
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) ycol[m][kk] = YF[m * 64 + kk * 8 + jj];
+            }
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+              float sacc = 0.f;
+#pragma unroll
+              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(drow[m][kk >> 2][kk & 3], ycol[m][kk], sacc);
+              TF[(8 * (m + 1) + ii) * FROW + 8 * m + jj] = -sacc;
+            }
+          }
+          wave_lds_sync();
+          // level 2: T[16:32][0:16] = -T22 (A21 T11), lane -> row 16 + i2, columns j2..j2+3
+          {
+            const int i2 = lane >> 2, j2 = (lane & 3) * 4;
+            f32x4 arow[4], tcol[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) arow[q] = *(const f32x4*)(AF + (16 + i2) * FROW + 4 * q);
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) tcol[kk] = *(const f32x4*)(TF + kk * FROW + j2);
+            f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) y[e] = __builtin_fmaf(arow[kk >> 2][kk & 3], tcol[kk][e], y[e]);
+            *(f32x4*)(YF + i2 * 20 + j2) = y;
+            wave_lds_sync();
+            f32x4 trow[4], ycol[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) trow[q] = *(const f32x4*)(TF + (16 + i2) * FROW + 16 + 4 * q);
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) ycol[kk] = *(const f32x4*)(YF + kk * 20 + j2);
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(trow[kk >> 2][kk & 3], ycol[kk][e], z[e]);
+            *(f32x4*)(TF + (16 + i2) * FROW + j2) = -z;
+          }
+          wave_lds_sync();
+          // T1 = T diag(beta e^gamma / ||k||) and T2 = T diag(beta) as operand fragments
+          // (lane = row l32, columns rho(v, h); lower triangle with the diagonal)
+          f32x16 tv1, tv2;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const f32x4 t4 = *(const f32x4*)(TF + l32 * FROW + 8 * m + 4 * h);
+            const f32x4 be4 = *(const f32x4*)(va + VA_BET + 8 * m + 4 * h);
+            const f32x4 eg4 = *(const f32x4*)(va + VA_EG + 8 * m + 4 * h);
+            const f32x4 rk4 = *(const f32x4*)(va + VA_RNK + 8 * m + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const bool in = 8 * m + 4 * ho + e <= lo;
+              tv1[4 * m + e] = in ? t4[e] * (be4[e] * eg4[e] * rk4[e]) : 0.f;
+              tv2[4 * m + e] = in ? t4[e] * be4[e] : 0.f;
+            }
+          }
+          F f1, f2;
+          acc_to_frag(tv1, f1);
+          acc_to_frag(tv2, f2);
+          bf16x8* t2d = T2f(gs, pn) + 2 * lane;
+          t2d[0] = f2.lo;
+          t2d[1] = f2.hi;
+          // W^T = K^T T1^T per 32-column slice of k: lane = row l32 of W, values = k columns
+          // 32 kt + rho(v, h), stored four consecutive columns at a time
+          bf16* const W = WB(gs, pn);
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) {
+            F fb;
+            lds_frag_tr(K + kt * 32, QROW, lane, fb);
+            f32x16 aw = zero16();
+            mma32(aw, fb, f1);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              bf16x4 w4;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w4[e] = (bf16)aw[4 * m + e];
+              *(bf16x4*)(W + l32 * QROW + kt * 32 + 8 * m + 4 * h) = w4;
+            }
+          }
+        } else {
+          // P^T = K Q^T: lane = query row l32, values = key rows rho(v, h); P_ij = mask(scale/||q_i||
+          // q_i . k^_j e^(gamma_i - gamma_j)), j <= i, with 1/||k_j|| applied to V' instead
+          const bf16* const Q = QB(gs, pn);
+          F fq[KT], fk[KT];
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) {
+            lds_frag(Q + l32 * QROW + kt * 32, h, fq[kt]);
+            lds_frag(K + l32 * QROW + kt * 32, h, fk[kt]);
+          }
+#pragma unroll
+          for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(va + VA_GAML + 8 * m + 4 * h);
+          f32x16 acc = zero16();
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) mma32(acc, fk[kt], fq[kt]);
+          __builtin_amdgcn_sched_group_barrier(0x100, 4 * KT + 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2 * KT, 0);
+          const float gi = va[VA_GAML + l32];
+          const float rqi = va[VA_RNQ + l32];
+          bf16* const P = PBf(gs, pn);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            bf16x4 p4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float val = rqi * acc[4 * m + e] * __builtin_amdgcn_exp2f(gi - gam4[m][e]);
+              p4[e] = (bf16)((8 * m + 4 * ho + e <= lo) ? val : 0.f);
+            }
+            *(bf16x4*)(P + l32 * TROW + 8 * m + 4 * h) = p4;
+          }
+          if (h == 0) vs[VS_EGQ + l32] = va[VA_EG + l32] * rqi;
+        }
+      }
+    }
+  }
+  } else {
+  // ---- state waves: the clean state of value columns [32u, 32u + 32)
+  f32x16 S[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) S[t] = zero16();
+  for (int c = -1; c < ntiles; ++c) {
+    __syncthreads();  // tile c-1's state phase and tile c's preparation are done
+    __syncthreads();  // the load phase is done
+    if (c >= 0) {
+      // ---------------------------------------------------------- state phase, tile c
+      const int pc = c & 1;
+      const int t0 = c * a.sub;
+      f32x16 accU[2], accWS[2], accQS[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        accU[s] = zero16();
+        accWS[s] = zero16();
+        accQS[s] = zero16();
+        F ft, fv;
+        const bf16x8* t2 = T2f(s, pc) + 2 * lane;
+        ft.lo = t2[0];
+        ft.hi = t2[1];
+        lds_frag_tr(VB(s) + u * 32, QROW, lane, fv);
+        mma32(accU[s], ft, fv);  // U = T2 V
+      }
+      // W S and Q S of both streams from the clean state before the tile
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        F sx;
+        acc_to_frag(S[kt], sx);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          F fw, fq;
+          lds_frag(WB(s, pc) + l32 * QROW + kt * 32, h, fw);
+          lds_frag(QB(s, pc) + l32 * QROW + kt * 32, h, fq);
+          mma32(accWS[s], fw, sx);
+          mma32(accQS[s], fq, sx);
+        }
+      }
+      const int rs = opaque(a.Hv * a.Dv);  // token stride of the outputs
+#pragma unroll
+      for (int si = 0; si < 2; ++si) {
+        const int s = 1 - si;  // noised first: the clean update below overwrites S
+        const float* vs = VS(s, pc);
+        // O = diag(e^gamma scale/||q||) Q S + P (V' / ||k||),  V' = U - W S
+        f32x16 vn, vk;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const f32x4 egq = *(const f32x4*)(vs + VS_EGQ + 8 * m + 4 * h);
+          const f32x4 rnk = *(const f32x4*)(vs + VS_RNK + 8 * m + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int v = 4 * m + e;
+            vn[v] = accU[s][v] - accWS[s][v];
+            vk[v] = vn[v] * rnk[e];
+            accQS[s][v] *= egq[e];
+          }
+        }
+        {
+          F fv, fp;
+          acc_to_frag(vk, fv);
+          lds_frag(PBf(s, pc) + l32 * TROW, h, fp);
+          mma32(accQS[s], fp, fv);
+        }
+        {
+          bf16* ob = (bf16*)a.s[s].out + ((long long)b * a.T + t0) * rs + (long long)hv * a.Dv + u * 32;
+          const unsigned lo2 = (unsigned)(4 * h * rs + l32);
+          if (a.sub == 32) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) (ob + (((v >> 2) << 3) + (v & 3)) * rs)[lo2] = (bf16)accQS[s][v];
+          } else {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int ru = ((v >> 2) << 3) + (v & 3);  // row = ru + 4h
+              if (ru + 4 * h < a.sub) (ob + ru * rs)[lo2] = (bf16)accQS[s][v];
+            }
+          }
+        }
+        if (s == 0) {
+          // S <- e^gamma_last S + K_raw^T (e^(gamma_last - gamma) / ||k|| V'), snapshot after the tile
+          const float lam = vs[VS_EG + 31];
+          f32x16 vd;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const f32x4 eglk = *(const f32x4*)(vs + VS_EGLK + 8 * m + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vd[4 * m + e] = vn[4 * m + e] * eglk[e];
+          }
+          F fd;
+          acc_to_frag(vd, fd);
+          F fk[KT];
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) lds_frag_tr(KB(0, pc) + kt * 32, QROW, lane, fk[kt]);
+          float* const sb = a.states ? a.states + (((long long)b * ntiles + c) * a.Hv + hv) * (128LL * 128) + u * 32 +
+                                           4 * h * 128 + l32
+                                     : nullptr;
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) S[kt][v] *= lam;
+            mma32(S[kt], fk[kt], fd);
+            if (sb) {
+#pragma unroll
+              for (int v = 0; v < 16; ++v)
+                __builtin_nontemporal_store(S[kt][v], sb + (32 * kt + ((v >> 2) << 3) + (v & 3)) * 128);
+            }
+          }
+        }
+      }
+    }
+  }
+  }
+}
+
 template <int DK, int DVW, bool BF16, bool FORK>
 static int launch_gdn(const GdnArgs& a, hipStream_t st) {
   const int nwin = (a.Dv + DVW - 1) / DVW;
@@ -725,6 +1251,15 @@ static int launch_gdn(const GdnArgs& a, hipStream_t st) {
   gdn_chunk_kernel<DK, DVW, BF16, FORK><<<dim3((unsigned)nblk), dim3(FORK ? 512 : 256), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "gdn launch: %s", hipGetErrorString(e));
+  return DLLM_OK;
+}
+
+static int launch_fork_pipe(const GdnArgs& a, hipStream_t st) {
+  const long long nblk = (long long)a.B * a.Hv;
+  if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "gdn: grid too large");
+  gdn_fork_pipe_kernel<<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "gdn fork launch: %s", hipGetErrorString(e));
   return DLLM_OK;
 }
 
@@ -862,5 +1397,7 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
   const int dkw = Dk <= 64 ? 64 : 128;
   a.vec_qk = aligned16(qkv0) && aligned16(qkvt) && st_ok && Dk == dkw;
   a.vec_v = aligned16(qkv0) && aligned16(qkvt) && st_ok && (Dv % window_for(dtype) == 0);
+  // full 128 x 128 heads with 16-byte rows: the pipelined kernel
+  if (dtype == DT_BF16 && Dk == 128 && Dv == 128 && a.vec_qk && a.vec_v) return launch_fork_pipe(a, (hipStream_t)stream);
   return dispatch_gdn(a, dtype, true, (hipStream_t)stream);
 }

@@ -735,16 +735,67 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
 // one prep wave. The arithmetic of every product and scaling is that of gdn_chunk_kernel, operand
 // for operand; W and P are produced as transposed MFMA products so that their LDS rows are written
 // four elements at a time.
+// Sum of squares of row l32 of a [32 x 128] bf16 operand held as four rho-ordered fragments (lane
+// (l32, h) holds 64 of the row's values): paired bf16 dot products into four fp32 partial sums,
+// then the other half of the row from lane l32 + 32 (or l32 - 32), so both lanes get the row total.
+__device__ __forceinline__ float row_sumsq(const Frag<true> (&f)[4]) {
+  float s[4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    float x = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bf16x2 lo = {f[kt].lo[2 * i], f[kt].lo[2 * i + 1]};
+      const bf16x2 hi = {f[kt].hi[2 * i], f[kt].hi[2 * i + 1]};
+      x = __builtin_amdgcn_fdot2_f32_bf16(lo, lo, x, false);
+      x = __builtin_amdgcn_fdot2_f32_bf16(hi, hi, x, false);
+    }
+    s[kt] = x;
+  }
+  const float half = (s[0] + s[1]) + (s[2] + s[3]);
+  // the other half from lane l ^ 32 (LDS crossbar permute); the sum is commutative, so the two
+  // lanes of a row hold bit-identical totals
+  const float other = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((__lane_id() ^ 32) << 2,
+                                                                            __builtin_bit_cast(int, half)));
+  return half + other;
+}
+
+// Pipelined-kernel operand convention. The state S is held with its rows (d) permuted inside each
+// 32-row slice: accumulator row rho(v, h) holds d = 16 h + v. Fed back as a B operand, value v of
+// lane (n, h) then carries d = 16 h + v, so every A operand contracted with it (W, Q) is read as 16
+// CONSECUTIVE d of its row: two 16-byte LDS reads instead of four 8-byte ones. Products whose two
+// operands both come from LDS rows (K K^T, K Q^T) use the same reads for both: the contraction pairs
+// equal d whatever the order.
+__device__ __forceinline__ void lds_frag_c(const bf16* base, int h, Frag<true>& f) {
+  const bf16* p = base + 16 * h;
+  f.lo = *(const bf16x8*)p;
+  f.hi = *(const bf16x8*)(p + 8);
+}
+// Transposed read (as lds_frag_tr) whose result lane r = 8 m + 4 h' + e receives column
+// 16 h' + 4 m + e of the 32-column slice: an A operand whose product rows come out in the permuted
+// d order above. The transpose read hands each group of four result lanes the four consecutive
+// columns one source lane addresses, so only the column-group addresses change.
+__device__ __forceinline__ void lds_frag_tr_d(const bf16* base, int row_stride, int lane, Frag<true>& f) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  const int s = lane & 15, j = s & 3;
+  const bf16* p = base + (4 * (lane >> 5) + (s >> 2)) * row_stride + 16 * (j & 1) + 4 * (2 * ((lane >> 4) & 1) + (j >> 1));
+  bf16x4 r[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    r[m] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 8 * m * row_stride));
+  f.lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+  f.hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 struct PipeSmem {
   static constexpr int DK = 128;
   static constexpr int QROW = DK + 8;          // bf16 row stride of q, k, W and v rows
-  static constexpr int TROW = 36;              // bf16 row stride of P
   static constexpr int FROW = 36;              // fp32 [32][32] scratch row stride
   static constexpr int ROWS = 32 * QROW * 2;   // one [32][QROW] bf16 buffer
-  static constexpr int PB = 32 * TROW * 2;
+  static constexpr int PB = 64 * 16 * 2;       // P operand fragment, lane-major
   static constexpr int T2B = 64 * 16 * 2;      // T2 operand fragment, lane-major
   static constexpr int VSB = 4 * 32 * 4;       // state-phase vectors: EGQ, RNK, EGLK, EG
-  static constexpr int VAB = 6 * 32 * 4;       // prep vectors: GAML, BET, EG, EGL, RNK, RNQ
+  static constexpr int VAB = 4 * 32 * 4;       // prep vectors: GAML, BET, EG, EGL
   static constexpr int FB = 32 * FROW * 4;
   static constexpr int YB = 16 * 20 * 4;
   // row buffers: Q[stream][parity], W[stream][parity], K clean [parity] + K noised (read only by
@@ -765,13 +816,13 @@ struct PipeSmem {
 };
 // vector slots (floats) inside the VS and VA blocks
 enum { VS_EGQ = 0, VS_RNK = 32, VS_EGLK = 64, VS_EG = 96 };
-enum { VA_GAML = 0, VA_BET = 32, VA_EG = 64, VA_EGL = 96, VA_RNK = 128, VA_RNQ = 160 };
+enum { VA_GAML = 0, VA_BET = 32, VA_EG = 64, VA_EGL = 96 };
 
 __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   using SM = PipeSmem;
   using F = Frag<true>;
   constexpr int KT = 4;
-  constexpr int QROW = SM::QROW, TROW = SM::TROW, FROW = SM::FROW;
+  constexpr int QROW = SM::QROW, FROW = SM::FROW;
   constexpr float LOG2E = 1.4426950408889634f;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
 
@@ -793,7 +844,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   auto WB = [&](int s, int p) { return (bf16*)(smem + SM::O_W + (2 * s + p) * SM::ROWS); };
   auto KB = [&](int s, int p) { return (bf16*)(smem + SM::O_K + (s == 0 ? p : 2) * SM::ROWS); };
   auto VB = [&](int s) { return (bf16*)(smem + SM::O_V + s * SM::ROWS); };
-  auto PBf = [&](int s, int p) { return (bf16*)(smem + SM::O_P + (2 * s + p) * SM::PB); };
+  auto PBf = [&](int s, int p) { return (bf16x8*)(smem + SM::O_P + (2 * s + p) * SM::PB); };
   auto T2f = [&](int s, int p) { return (bf16x8*)(smem + SM::O_T2 + (2 * s + p) * SM::T2B); };
   auto VS = [&](int s, int p) { return (float*)(smem + SM::O_VS + (2 * s + p) * SM::VSB); };
   auto VA = [&](int s) { return (float*)(smem + SM::O_VA + s * SM::VAB); };
@@ -801,32 +852,31 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   auto TFf = [&](int s) { return (float*)(smem + SM::O_TF + s * SM::FB); };
   auto YFf = [&](int s) { return (float*)(smem + SM::O_YF + s * SM::YB); };
 
-  // ---- prep waves: loads. Thread (row lr, segment lseg) of the 256 prep threads holds, for both
-  // streams, q and k columns [8 lseg, +8) and [64 + 8 lseg, +8) of tile row lr, and v likewise.
-  const int gt = tid & 255;
-  const int lr = gt >> 3, lseg = gt & 7;
-  const bool lreal = lr < a.sub;  // rows >= sub are zero padding (loaded from row 0, zeroed on use)
-  const int e0 = lseg * 8, e1 = 64 + lseg * 8;
-  bf16x8 rq[2][2], rk[2][2], rv[2][2];
+  // ---- prep waves: loads. The P wave of each stream (wave 5 / 7) loads that stream's q, k and v
+  // rows, so that the G waves, whose preparation chain is the longest, issue no row loads: lane
+  // (row group lr0, segment lseg) holds columns [8 lseg, +8) of tile rows lr0 + 4 i, i = 0..7
+  // (sixteen lanes per row: every load and LDS write instruction covers four whole 256-byte rows,
+  // so the LDS writes are free of bank conflicts). The G waves load g and beta.
+  const int lr0 = lane >> 4, lseg = lane & 15;
+  const int e0 = lseg * 8;
+  bf16x8 rq[8], rk[8], rv[8];
   float rg = 0.f, rb = 0.f;
   auto issue_loads = [&](int tq, int tvv) {  // q/k (and g, beta) of tile tq, v of tile tvv; -1 = none
+    if (prep && !isG) {
+      const GdnStream& st = a.s[gs];
+      const bf16* const qb = (const bf16*)st.q + b * a.q_sb + (long long)hk * a.q_sh + e0;
+      const bf16* const kb = (const bf16*)st.k + b * a.k_sb + (long long)hk * a.k_sh + e0;
+      const bf16* const vb = (const bf16*)st.v + b * a.v_sb + (long long)hv * a.v_sh + e0;
+      // unconditional loads (a tile index of -1 reloads tile 0, unused), so that the compiler
+      // counts them exactly and the load phase waits only for the row it writes
+      const int tqq = tq < 0 ? 0 : tq, tvq = tvv < 0 ? 0 : tvv;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const GdnStream& st = a.s[s];
-      if (tq >= 0) {
-        const int tok = tq * a.sub + (lreal ? lr : 0);
-        const bf16* qr = (const bf16*)st.q + b * a.q_sb + (long long)hk * a.q_sh + tok * a.q_st;
-        const bf16* kr = (const bf16*)st.k + b * a.k_sb + (long long)hk * a.k_sh + tok * a.k_st;
-        rq[s][0] = *(const bf16x8*)(qr + e0);
-        rq[s][1] = *(const bf16x8*)(qr + e1);
-        rk[s][0] = *(const bf16x8*)(kr + e0);
-        rk[s][1] = *(const bf16x8*)(kr + e1);
-      }
-      if (tvv >= 0) {
-        const int tok = tvv * a.sub + (lreal ? lr : 0);
-        const bf16* vr = (const bf16*)st.v + b * a.v_sb + (long long)hv * a.v_sh + tok * a.v_st;
-        rv[s][0] = *(const bf16x8*)(vr + e0);
-        rv[s][1] = *(const bf16x8*)(vr + e1);
+      for (int i = 0; i < 8; ++i) {
+        const int r = lr0 + 4 * i;
+        const int rr = r < a.sub ? r : 0;  // rows >= sub are zero padding (loaded from row 0, zeroed on use)
+        rq[i] = *(const bf16x8*)(qb + (tqq * a.sub + rr) * a.q_st);
+        rk[i] = *(const bf16x8*)(kb + (tqq * a.sub + rr) * a.k_st);
+        rv[i] = *(const bf16x8*)(vb + (tvq * a.sub + rr) * a.v_st);
       }
     }
     // g and beta: every lane loads (padding rows from the last real row, zeroed on use), so that
@@ -844,6 +894,8 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   // neither role's registers (prefetched inputs, the state) are held live through the other.
   const bf16x8 vzero = {};
   if (prep) {
+  // the G waves carry the longest chain of a tile: the SIMD arbiter serves them first
+  if (isG) __builtin_amdgcn_s_setprio(2);
   issue_loads(0, -1);
   for (int c = -1; c < ntiles; ++c) {
     const int lo = opaque_v(l32), ho = opaque_v(h);  // lane indices for masks (see opaque_v)
@@ -851,37 +903,34 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
     // ------------------------------------------------------------ load phase
     {
       const int pn = (c + 1) & 1;
-      if (c + 1 < ntiles) {
+      // P waves: raw q and k rows of tile c + 1 and v rows of tile c of their stream; rows >= sub
+      // are written as zeros (whole tiles take the branch without selects)
+      if (!isG) {
+        bf16* const qb = QB(gs, pn) + e0;
+        bf16* const kb = KB(gs, pn) + e0;
+        bf16* const vb = VB(gs) + e0;
+        if (a.sub == 32 && c >= 0 && c + 1 < ntiles) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          bf16x8 xq[2], xk[2];
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            xq[i] = lreal ? rq[s][i] : vzero;
-            xk[i] = lreal ? rk[s][i] : vzero;
+          for (int i = 0; i < 8; ++i) {
+            const int r = lr0 + 4 * i;
+            *(bf16x8*)(qb + r * QROW) = rq[i];
+            *(bf16x8*)(kb + r * QROW) = rk[i];
+            *(bf16x8*)(vb + r * QROW) = rv[i];
           }
-          bf16* q = QB(s, pn) + lr * QROW;
-          bf16* k = KB(s, pn) + lr * QROW;
-          *(bf16x8*)(q + e0) = xq[0];
-          *(bf16x8*)(q + e1) = xq[1];
-          *(bf16x8*)(k + e0) = xk[0];
-          *(bf16x8*)(k + e1) = xk[1];
-          // q and k row norms: fp32 sums of squares over the row's 8 threads (DPP)
-          float ss = 0.f, sk = 0.f;
+        } else {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float x = to_f32(xq[i >> 3][i & 7]);
-            const float y = to_f32(xk[i >> 3][i & 7]);
-            ss = __builtin_fmaf(x, x, ss);
-            sk = __builtin_fmaf(y, y, sk);
-          }
-          ss = dpp_sum8(ss);
-          sk = dpp_sum8(sk);
-          if (lseg == 0) {
-            VA(s)[VA_RNQ + lr] = a.l2norm ? a.scale * rsqrtf(ss + 1e-6f) : a.scale;
-            VA(s)[VA_RNK + lr] = a.l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
+          for (int i = 0; i < 8; ++i) {
+            const int r = lr0 + 4 * i;
+            const bool real = r < a.sub;
+            if (c + 1 < ntiles) {
+              *(bf16x8*)(qb + r * QROW) = real ? rq[i] : vzero;
+              *(bf16x8*)(kb + r * QROW) = real ? rk[i] : vzero;
+            }
+            if (c >= 0) *(bf16x8*)(vb + r * QROW) = real ? rv[i] : vzero;
           }
         }
+      }
+      if (c + 1 < ntiles) {
         // cumulative decay of the next tile: inclusive scan of g over its rows (lanes 0..31)
         if (isG) {
           const bool greal = h == 0 && l32 < a.sub;
@@ -900,14 +949,6 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
             va[VA_EG + l32] = __builtin_amdgcn_exp2f(gam * LOG2E);
             va[VA_EGL + l32] = __builtin_amdgcn_exp2f((gall - gam) * LOG2E);
           }
-        }
-      }
-      if (c >= 0) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          bf16* v = VB(s) + lr * QROW;
-          *(bf16x8*)(v + e0) = lreal ? rv[s][0] : vzero;
-          *(bf16x8*)(v + e1) = lreal ? rv[s][1] : vzero;
         }
       }
     }
@@ -930,22 +971,30 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           f32x16 acc = zero16();
           F fa[KT];
 #pragma unroll
-          for (int kt = 0; kt < KT; ++kt) lds_frag(K + l32 * QROW + kt * 32, h, fa[kt]);
+          for (int kt = 0; kt < KT; ++kt) lds_frag_c(K + l32 * QROW + kt * 32, h, fa[kt]);
 #pragma unroll
           for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(va + VA_GAML + 8 * m + 4 * h);
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt) mma32(acc, fa[kt], fa[kt]);
           __builtin_amdgcn_sched_group_barrier(0x100, 2 * KT + 4, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 2 * KT, 0);
+          // k row norms from the Gram operands while the products run: lane (l32, h) holds half
+          // of row l32; the row's 1/||k|| goes to the state vectors and comes back as row vectors
+          const float rj = a.l2norm ? rsqrtf(row_sumsq(fa) + 1e-6f) : 1.f;
+          const float eglj = va[VA_EGL + l32];
+          if (h == 0) {
+            vs[VS_EGLK + l32] = eglj * rj;
+            vs[VS_RNK + l32] = rj;
+            vs[VS_EG + l32] = va[VA_EG + l32];
+          }
+          wave_lds_sync();
           const float gj = va[VA_GAML + l32];
           f32x4 bet4[4], rnk4[4];
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
             bet4[m] = *(const f32x4*)(va + VA_BET + 8 * m + 4 * h);
-            rnk4[m] = *(const f32x4*)(va + VA_RNK + 8 * m + 4 * h);
+            rnk4[m] = *(const f32x4*)(vs + VS_RNK + 8 * m + 4 * h);
           }
-          const float rj = va[VA_RNK + l32];
-          const float eglj = va[VA_EGL + l32];
 #pragma unroll
           for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -955,11 +1004,6 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
                                 __builtin_amdgcn_exp2f(gam4[m][e] - gj);
               AF[i * FROW + l32] = (lo < 8 * m + 4 * ho + e) ? val : 0.f;
             }
-          if (h == 0) {
-            vs[VS_EGLK + l32] = eglj * rj;
-            vs[VS_RNK + l32] = rj;
-            vs[VS_EG + l32] = va[VA_EG + l32];
-          }
           wave_lds_sync();
           // level 0: four 8x8 diagonal blocks, one column per lane (lanes 0..31); lanes of odd
           // blocks also clear the block above (read as zero by level 2)
@@ -1063,11 +1107,11 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
             const f32x4 t4 = *(const f32x4*)(TF + l32 * FROW + 8 * m + 4 * h);
             const f32x4 be4 = *(const f32x4*)(va + VA_BET + 8 * m + 4 * h);
             const f32x4 eg4 = *(const f32x4*)(va + VA_EG + 8 * m + 4 * h);
-            const f32x4 rk4 = *(const f32x4*)(va + VA_RNK + 8 * m + 4 * h);
+            const f32x4 rk4 = *(const f32x4*)(vs + VS_RNK + 8 * m + 4 * h);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const bool in = 8 * m + 4 * ho + e <= lo;
-              tv1[4 * m + e] = in ? t4[e] * (be4[e] * eg4[e] * rk4[e]) : 0.f;
+              tv1[4 * m + e] = in ? -(t4[e] * (be4[e] * eg4[e] * rk4[e])) : 0.f;  // -T1: W is stored negated
               tv2[4 * m + e] = in ? t4[e] * be4[e] : 0.f;
             }
           }
@@ -1077,22 +1121,19 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           bf16x8* t2d = T2f(gs, pn) + 2 * lane;
           t2d[0] = f2.lo;
           t2d[1] = f2.hi;
-          // W^T = K^T T1^T per 32-column slice of k: lane = row l32 of W, values = k columns
-          // 32 kt + rho(v, h), stored four consecutive columns at a time
+          // W^T = K^T T1^T per 32-column slice of k with the permuted transposed read: lane = row
+          // l32 of W, value v = k column 32 kt + 16 h + v, stored as two 16-byte runs
           bf16* const W = WB(gs, pn);
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt) {
-            F fb;
-            lds_frag_tr(K + kt * 32, QROW, lane, fb);
+            F fb, fwo;
+            lds_frag_tr_d(K + kt * 32, QROW, lane, fb);
             f32x16 aw = zero16();
             mma32(aw, fb, f1);
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-              bf16x4 w4;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) w4[e] = (bf16)aw[4 * m + e];
-              *(bf16x4*)(W + l32 * QROW + kt * 32 + 8 * m + 4 * h) = w4;
-            }
+            acc_to_frag(aw, fwo);
+            bf16x8* const wr = (bf16x8*)(W + l32 * QROW + kt * 32 + 16 * h);
+            wr[0] = fwo.lo;
+            wr[1] = fwo.hi;
           }
         } else {
           // P^T = K Q^T: lane = query row l32, values = key rows rho(v, h); P_ij = mask(scale/||q_i||
@@ -1101,8 +1142,8 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           F fq[KT], fk[KT];
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt) {
-            lds_frag(Q + l32 * QROW + kt * 32, h, fq[kt]);
-            lds_frag(K + l32 * QROW + kt * 32, h, fk[kt]);
+            lds_frag_c(Q + l32 * QROW + kt * 32, h, fq[kt]);
+            lds_frag_c(K + l32 * QROW + kt * 32, h, fk[kt]);
           }
 #pragma unroll
           for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(va + VA_GAML + 8 * m + 4 * h);
@@ -1112,18 +1153,23 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           __builtin_amdgcn_sched_group_barrier(0x100, 4 * KT + 4, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 2 * KT, 0);
           const float gi = va[VA_GAML + l32];
-          const float rqi = va[VA_RNQ + l32];
-          bf16* const P = PBf(gs, pn);
+          // scale / ||q|| of query row l32 from this lane's half of the row and the other half's
+          const float rqi = a.l2norm ? a.scale * rsqrtf(row_sumsq(fq) + 1e-6f) : a.scale;
+          // P is kept as the A operand fragment of P V' (lane = query row, values = key rows in
+          // rho order: the accumulator's own layout), lane-major
+          f32x16 pv;
 #pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            bf16x4 p4;
+          for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float val = rqi * acc[4 * m + e] * __builtin_amdgcn_exp2f(gi - gam4[m][e]);
-              p4[e] = (bf16)((8 * m + 4 * ho + e <= lo) ? val : 0.f);
+              pv[4 * m + e] = (8 * m + 4 * ho + e <= lo) ? val : 0.f;
             }
-            *(bf16x4*)(P + l32 * TROW + 8 * m + 4 * h) = p4;
-          }
+          F fpo;
+          acc_to_frag(pv, fpo);
+          bf16x8* const pd = PBf(gs, pn) + 2 * lane;
+          pd[0] = fpo.lo;
+          pd[1] = fpo.hi;
           if (h == 0) vs[VS_EGQ + l32] = va[VA_EG + l32] * rqi;
         }
       }
@@ -1141,33 +1187,53 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
       // ---------------------------------------------------------- state phase, tile c
       const int pc = c & 1;
       const int t0 = c * a.sub;
-      f32x16 accU[2], accWS[2], accQS[2];
+      // V' = U - W S accumulates in one tile per stream: U = T2 V first, then the products with
+      // the negated W rows the preparation stored
+      f32x16 accV[2], accQS[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        accU[s] = zero16();
-        accWS[s] = zero16();
+        accV[s] = zero16();
         accQS[s] = zero16();
         F ft, fv;
         const bf16x8* t2 = T2f(s, pc) + 2 * lane;
         ft.lo = t2[0];
         ft.hi = t2[1];
         lds_frag_tr(VB(s) + u * 32, QROW, lane, fv);
-        mma32(accU[s], ft, fv);  // U = T2 V
+        mma32(accV[s], ft, fv);  // U = T2 V
       }
-      // W S and Q S of both streams from the clean state before the tile
+      // -W S and Q S of both streams from the clean state before the tile; the W and Q fragments
+      // of slice kt + 1 are read while the products of slice kt run
+      F fw[2][2], fq[2][2];  // [slice parity][stream]
+      auto read_wq = [&](int kt) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          lds_frag_c(WB(s, pc) + l32 * QROW + kt * 32, h, fw[kt & 1][s]);
+          lds_frag_c(QB(s, pc) + l32 * QROW + kt * 32, h, fq[kt & 1][s]);
+        }
+      };
+      read_wq(0);
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
         F sx;
         acc_to_frag(S[kt], sx);
+        if (kt + 1 < KT) read_wq(kt + 1);
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          F fw, fq;
-          lds_frag(WB(s, pc) + l32 * QROW + kt * 32, h, fw);
-          lds_frag(QB(s, pc) + l32 * QROW + kt * 32, h, fq);
-          mma32(accWS[s], fw, sx);
-          mma32(accQS[s], fq, sx);
+          mma32(accV[s], fw[kt & 1][s], sx);
+          mma32(accQS[s], fq[kt & 1][s], sx);
         }
       }
+      // issue order: the U operand reads, slice 0's reads, the U products, then each slice's
+      // products behind the next slice's reads (keeps eight LDS reads in flight per wave)
+      __builtin_amdgcn_sched_group_barrier(0x100, 12, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+#pragma unroll
+      for (int kt = 0; kt + 1 < KT; ++kt) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
       const int rs = opaque(a.Hv * a.Dv);  // token stride of the outputs
 #pragma unroll
       for (int si = 0; si < 2; ++si) {
@@ -1182,7 +1248,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int v = 4 * m + e;
-            vn[v] = accU[s][v] - accWS[s][v];
+            vn[v] = accV[s][v];
             vk[v] = vn[v] * rnk[e];
             accQS[s][v] *= egq[e];
           }
@@ -1190,7 +1256,9 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
         {
           F fv, fp;
           acc_to_frag(vk, fv);
-          lds_frag(PBf(s, pc) + l32 * TROW, h, fp);
+          const bf16x8* const pp = PBf(s, pc) + 2 * lane;
+          fp.lo = pp[0];
+          fp.hi = pp[1];
           mma32(accQS[s], fp, fv);
         }
         {
@@ -1221,9 +1289,10 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           acc_to_frag(vd, fd);
           F fk[KT];
 #pragma unroll
-          for (int kt = 0; kt < KT; ++kt) lds_frag_tr(KB(0, pc) + kt * 32, QROW, lane, fk[kt]);
+          for (int kt = 0; kt < KT; ++kt) lds_frag_tr_d(KB(0, pc) + kt * 32, QROW, lane, fk[kt]);
+          // accumulator row rho(v, h) of slice kt is state row 32 kt + 16 h + v
           float* const sb = a.states ? a.states + (((long long)b * ntiles + c) * a.Hv + hv) * (128LL * 128) + u * 32 +
-                                           4 * h * 128 + l32
+                                           16 * h * 128 + l32
                                      : nullptr;
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt) {
@@ -1233,7 +1302,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
             if (sb) {
 #pragma unroll
               for (int v = 0; v < 16; ++v)
-                __builtin_nontemporal_store(S[kt][v], sb + (32 * kt + ((v >> 2) << 3) + (v & 3)) * 128);
+                __builtin_nontemporal_store(S[kt][v], sb + (32 * kt + v) * 128);
             }
           }
         }

@@ -21,14 +21,17 @@ namespace dllm {
 
 template <typename T, int N> struct alignas(sizeof(T) * N) VecN { T v[N]; };
 
-template <typename TX, typename TW, int K, int VEC>
-__global__ __launch_bounds__(256) void conv_fork_kernel(
+// BLK > 0 fixes the block length at compile time: the row loop unrolls completely and the K-1-row
+// history stays in registers without moves between rows.
+template <typename TX, typename TW, int K, int VEC, int BLK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BLK > 0 ? 5 : 1, BLK > 0 ? 5 : 8))) void conv_fork_kernel(
     const TX* __restrict__ raw0, const TX* __restrict__ rawt, const TW* __restrict__ w,
     const TW* __restrict__ bias, TX* __restrict__ y0, TX* __restrict__ yt, TX* __restrict__ tails,
     int L, int Cd, int block, int cold_noised) {
   const int cg = blockIdx.x * blockDim.x + threadIdx.x;  // channel group
   const int c0 = cg * VEC;
   if (c0 >= Cd) return;
+  if (BLK > 0) block = BLK;
   const int kblk = blockIdx.y;
   const int b = blockIdx.z;
   const int nb = L / block;
@@ -67,15 +70,18 @@ __global__ __launch_bounds__(256) void conv_fork_kernel(
   if (tails) {
     TX* dst = tails + ((long long)fork_row(b, kblk, nb) * Cd + c0) * (K - 1);
     constexpr int TN = VEC * (K - 1);
-    constexpr int EPV16 = 16 / (int)sizeof(TX);
-    if constexpr (TN % EPV16 == 0) {  // whole 16-byte stores (aligned: c0 is a multiple of VEC)
-      typedef VecN<TX, EPV16> V16t;
+    // widest store dividing the run: the run starts at element c0 * (K - 1), c0 a multiple of VEC
+    constexpr int TB = TN * (int)sizeof(TX);
+    constexpr int SB = TB % 16 == 0 ? 16 : TB % 8 == 0 ? 8 : 0;
+    if constexpr (SB > 0) {
+      constexpr int EPS = SB / (int)sizeof(TX);
+      typedef VecN<TX, EPS> Vst;
 #pragma unroll
-      for (int i = 0; i < TN / EPV16; ++i) {
-        V16t v;
+      for (int i = 0; i < TN / EPS; ++i) {
+        Vst v;
 #pragma unroll
-        for (int e = 0; e < EPV16; ++e) v.v[e] = tl[i * EPV16 + e];
-        *(V16t*)(dst + i * EPV16) = v;
+        for (int e = 0; e < EPS; ++e) v.v[e] = tl[i * EPS + e];
+        *(Vst*)(dst + i * EPS) = v;
       }
     } else {
 #pragma unroll
@@ -169,25 +175,39 @@ static int launch_fork(const void* raw0, const void* rawt, const void* w, const 
   const bool vec_ok = (Cd % V == 0) && ((uintptr_t)raw0 % 16 == 0) && ((uintptr_t)rawt % 16 == 0) &&
                       ((uintptr_t)y0 % 16 == 0) && ((uintptr_t)yt % 16 == 0) &&
                       ((uintptr_t)tails % 16 == 0);  // tails rows of VEC*(K-1) elements are 16-byte multiples
-  if (K == 4 && vec_ok) {
+  bool done = false;
+  if constexpr (V == 8) {
+    if (K == 4 && vec_ok && block == 32) {
+      // 8-byte channel groups at five resident waves per SIMD: at the 27B-class shape (B = 4,
+      // L = 4096, conv_dim = 10240) the 20480 waves are exactly four rounds of the chip's slots
+      const int groups = Cd / 4;
+      dim3 grid((groups + 255) / 256, nb, B);
+      conv_fork_kernel<TX, TW, 4, 4, 32><<<grid, 256, 0, st>>>(
+          (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
+          Cd, block, cold);
+      done = true;
+    }
+  }
+  if (done) {
+  } else if (K == 4 && vec_ok) {
     const int groups = Cd / V;
     dim3 grid((groups + 255) / 256, nb, B);
-    conv_fork_kernel<TX, TW, 4, V><<<grid, 256, 0, st>>>(
+    conv_fork_kernel<TX, TW, 4, V, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
         Cd, block, cold);
   } else if (K == 4) {
     dim3 grid((Cd + 255) / 256, nb, B);
-    conv_fork_kernel<TX, TW, 4, 1><<<grid, 256, 0, st>>>(
+    conv_fork_kernel<TX, TW, 4, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
         Cd, block, cold);
   } else if (K == 2) {
     dim3 grid((Cd + 255) / 256, nb, B);
-    conv_fork_kernel<TX, TW, 2, 1><<<grid, 256, 0, st>>>(
+    conv_fork_kernel<TX, TW, 2, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
         Cd, block, cold);
   } else if (K == 3) {
     dim3 grid((Cd + 255) / 256, nb, B);
-    conv_fork_kernel<TX, TW, 3, 1><<<grid, 256, 0, st>>>(
+    conv_fork_kernel<TX, TW, 3, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
         Cd, block, cold);
   } else {

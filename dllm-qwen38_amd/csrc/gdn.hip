@@ -720,21 +720,23 @@ __global__ __launch_bounds__(FORK ? 512 : 256) void gdn_chunk_kernel(GdnArgs a) 
 // ============================================================================================
 // Pipelined state fork (bf16, Dk = Dv = 128, one workgroup per (sequence, value head)).
 //
-// The recurrence S <- e^gamma_last S + K^T (U - W S) is the only sequential dependency of a tile;
-// the Gram products, the inverse T = (I + A)^-1, W = T1 K and P = mask(Q K^T) depend on the tile's
-// inputs alone. Here they are formed one tile AHEAD, beside the state work of the current tile:
+// The recurrence S <- e^gamma_last S + K~^T V', V' = U - T1 K S, is the only sequential
+// dependency of a tile; the Gram products, the inverse T = (I + A)^-1 and its scaled operands
+// T1, T2 (U = T2 V), and P = mask(Q K^T) depend on the tile's inputs alone. They are formed one
+// tile AHEAD, beside the state work of the current tile:
 //   waves 0-3 (state waves) each own 32 value columns of BOTH streams. They hold the clean state of
-//            their columns in MFMA accumulators and, per tile, compute the noised outputs from it
-//            (the clean state before the tile: the fork), then the clean outputs and the update.
-//   waves 4-7 (prep waves) load every input and prepare the next tile: wave 4 / 6 (clean / noised)
-//            K K^T, the decay/beta mask A, T by blocked forward substitution in fp32, W and the T2
-//            operand; wave 5 / 7 P with the q norms and decay folded in.
-// One tile = two barriers: a load phase (prep waves store the next tile's raw q/k and this tile's
-// v rows into LDS) and a compute phase (state(c) on waves 0-3 beside prep(c+1) on waves 4-7), with
-// every operand the two exchange double-buffered by tile parity. Each SIMD runs one state wave and
-// one prep wave. The arithmetic of every product and scaling is that of gdn_chunk_kernel, operand
-// for operand; W and P are produced as transposed MFMA products so that their LDS rows are written
-// four elements at a time.
+//            their columns in MFMA accumulators and, per tile, form K S and Q S of both streams
+//            from it, then V' = T2 V - T1 (K S) (W = T1 K is never formed), the noised outputs
+//            (the clean state before the tile: the fork), the clean outputs and the update.
+//   waves 4 / 6 (G waves, clean / noised) prepare the next tile: K K^T with the k norms, the
+//            decay/beta mask A, T by blocked forward substitution in fp32, the T1 and T2 operand
+//            fragments.
+//   waves 5 / 7 (P waves, clean / noised) prepare P with the q norms and decay folded in, and
+//            own every row load of their stream: they store the next tile's v rows (v is
+//            double-buffered) and the q and k rows of the tile after next, the latter into the
+//            buffers of the current tile once the state waves have read them (an LDS counter).
+// One barrier per tile; every operand the roles exchange is double-buffered by tile parity. Each
+// SIMD runs one state wave beside one G or P wave.
 // Sum of squares of row l32 of a [32 x 128] bf16 operand held as four rho-ordered fragments (lane
 // (l32, h) holds 64 of the row's values): paired bf16 dot products into four fp32 partial sums,
 // then the other half of the row from lane l32 + 32 (or l32 - 32), so both lanes get the row total.
@@ -795,28 +797,31 @@ struct PipeSmem {
   static constexpr int PB = 64 * 16 * 2;       // P operand fragment, lane-major
   static constexpr int T2B = 64 * 16 * 2;      // T2 operand fragment, lane-major
   static constexpr int VSB = 4 * 32 * 4;       // state-phase vectors: EGQ, RNK, EGLK, EG
-  static constexpr int VAB = 4 * 32 * 4;       // prep vectors: GAML, BET, EG, EGL
+  static constexpr int VAB = 4 * 32 * 4;       // G-wave vectors: GAML, BET, EG, EGL
+  static constexpr int VPB = 2 * 32 * 4;       // P-wave vectors: GAML, EG
   static constexpr int FB = 32 * FROW * 4;
   static constexpr int YB = 16 * 20 * 4;
-  // row buffers: Q[stream][parity], W[stream][parity], K clean [parity] + K noised (read only by
-  // the preparation, which finishes before the next load phase), V[stream]
+  // row buffers Q, K, V and operand fragments P, T1, T2, all [stream][parity]
   static constexpr int O_Q = 0;
-  static constexpr int O_W = O_Q + 4 * ROWS;
-  static constexpr int O_K = O_W + 4 * ROWS;
-  static constexpr int O_V = O_K + 3 * ROWS;
-  static constexpr int O_P = O_V + 2 * ROWS;
-  static constexpr int O_T2 = O_P + 4 * PB;
+  static constexpr int O_K = O_Q + 4 * ROWS;
+  static constexpr int O_V = O_K + 4 * ROWS;
+  static constexpr int O_P = O_V + 4 * ROWS;
+  static constexpr int O_T1 = O_P + 4 * PB;
+  static constexpr int O_T2 = O_T1 + 4 * T2B;
   static constexpr int O_VS = O_T2 + 4 * T2B;
   static constexpr int O_VA = O_VS + 4 * VSB;
-  static constexpr int O_AF = O_VA + 2 * VAB;
+  static constexpr int O_VP = O_VA + 2 * VAB;
+  static constexpr int O_AF = O_VP + 2 * VPB;
   static constexpr int O_TF = O_AF + 2 * FB;
   static constexpr int O_YF = O_TF + 2 * FB;
-  static constexpr int TOTAL = O_YF + 2 * YB;
+  static constexpr int O_FLAG = O_YF + 2 * YB;  // count of state waves done reading a tile's rows
+  static constexpr int TOTAL = O_FLAG + 16;
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
 };
 // vector slots (floats) inside the VS and VA blocks
 enum { VS_EGQ = 0, VS_RNK = 32, VS_EGLK = 64, VS_EG = 96 };
 enum { VA_GAML = 0, VA_BET = 32, VA_EG = 64, VA_EGL = 96 };
+enum { VP_GAML = 0, VP_EG = 32 };
 
 __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   using SM = PipeSmem;
@@ -841,13 +846,15 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   const int ntiles = a.T / a.sub;
 
   auto QB = [&](int s, int p) { return (bf16*)(smem + SM::O_Q + (2 * s + p) * SM::ROWS); };
-  auto WB = [&](int s, int p) { return (bf16*)(smem + SM::O_W + (2 * s + p) * SM::ROWS); };
-  auto KB = [&](int s, int p) { return (bf16*)(smem + SM::O_K + (s == 0 ? p : 2) * SM::ROWS); };
-  auto VB = [&](int s) { return (bf16*)(smem + SM::O_V + s * SM::ROWS); };
+  auto KB = [&](int s, int p) { return (bf16*)(smem + SM::O_K + (2 * s + p) * SM::ROWS); };
+  auto T1f = [&](int s, int p) { return (bf16x8*)(smem + SM::O_T1 + (2 * s + p) * SM::T2B); };
+  auto VB = [&](int s, int p) { return (bf16*)(smem + SM::O_V + (2 * s + p) * SM::ROWS); };
   auto PBf = [&](int s, int p) { return (bf16x8*)(smem + SM::O_P + (2 * s + p) * SM::PB); };
   auto T2f = [&](int s, int p) { return (bf16x8*)(smem + SM::O_T2 + (2 * s + p) * SM::T2B); };
   auto VS = [&](int s, int p) { return (float*)(smem + SM::O_VS + (2 * s + p) * SM::VSB); };
   auto VA = [&](int s) { return (float*)(smem + SM::O_VA + s * SM::VAB); };
+  auto VP = [&](int s) { return (float*)(smem + SM::O_VP + s * SM::VPB); };
+  unsigned* const flag = (unsigned*)(smem + SM::O_FLAG);
   auto AFf = [&](int s) { return (float*)(smem + SM::O_AF + s * SM::FB); };
   auto TFf = [&](int s) { return (float*)(smem + SM::O_TF + s * SM::FB); };
   auto YFf = [&](int s) { return (float*)(smem + SM::O_YF + s * SM::YB); };
@@ -860,7 +867,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   const int lr0 = lane >> 4, lseg = lane & 15;
   const int e0 = lseg * 8;
   bf16x8 rq[8], rk[8], rv[8];
-  float rg = 0.f, rb = 0.f;
+  float rg = 0.f, rb = 0.f, rgp = 0.f;
   auto issue_loads = [&](int tq, int tvv) {  // q/k (and g, beta) of tile tq, v of tile tvv; -1 = none
     if (prep && !isG) {
       const GdnStream& st = a.s[gs];
@@ -878,6 +885,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
         rk[i] = *(const bf16x8*)(kb + (tqq * a.sub + rr) * a.k_st);
         rv[i] = *(const bf16x8*)(vb + (tvq * a.sub + rr) * a.v_st);
       }
+      rgp = st.g[b * a.g_sb + (long long)hv * a.g_sh + (tqq * a.sub + min(l32, a.sub - 1)) * a.g_st];
     }
     // g and beta: every lane loads (padding rows from the last real row, zeroed on use), so that
     // no constant is ever written to these registers while a load into them may be in flight
@@ -890,70 +898,77 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
     }
   };
 
-  // The two roles run separate loops with the same barrier sequence (two per tile), so that
-  // neither role's registers (prefetched inputs, the state) are held live through the other.
+  // inclusive scan of g over the tile's rows (lanes 0..31 and, in `both`, 32..63 alike): the
+  // cumulative decay gamma of row l32; rows >= sub contribute zero
+  auto gamma_scan = [&](float g, bool both) {
+    float x = ((both || h == 0) && l32 < a.sub) ? g : 0.f;
+    x += dpp_mov<0x111>(x);  // row_shr:1
+    x += dpp_mov<0x112>(x);  // row_shr:2
+    x += dpp_mov<0x114>(x);  // row_shr:4
+    x += dpp_mov<0x118>(x);  // row_shr:8
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
+    return x;
+  };
   const bf16x8 vzero = {};
+  // raw rows of one tile from this P wave's registers into LDS; rows >= sub are written as zeros
+  // (whole tiles take the branch without selects)
+  auto put_rows = [&](bf16* dst, const bf16x8* src) {
+    dst += e0;
+    if (a.sub == 32) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *(bf16x8*)(dst + (lr0 + 4 * i) * QROW) = src[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = lr0 + 4 * i;
+        *(bf16x8*)(dst + r * QROW) = r < a.sub ? src[i] : vzero;
+      }
+    }
+  };
+
+  // One barrier per tile. In the phase of tile c, the state waves run tile c; the G and P waves
+  // prepare tile c + 1 from its rows, which are in LDS since the phase before; the P waves then
+  // store tile c + 1's v rows (v is double-buffered) and, once every state wave has read tile c's
+  // q and k rows (the LDS counter `flag`), tile c + 2's q and k rows into the buffers of tile c.
+  // The roles run separate loops with the same barrier sequence, so that neither role's registers
+  // (prefetched rows, the state) are held live through the other.
+  if (tid == 0) *flag = 0u;
   if (prep) {
   // the G waves carry the longest chain of a tile: the SIMD arbiter serves them first
   if (isG) __builtin_amdgcn_s_setprio(2);
   issue_loads(0, -1);
+  if (!isG) {
+    put_rows(QB(gs, 0), rq);
+    put_rows(KB(gs, 0), rk);
+  }
   for (int c = -1; c < ntiles; ++c) {
     const int lo = opaque_v(l32), ho = opaque_v(h);  // lane indices for masks (see opaque_v)
     __syncthreads();  // tile c-1's state phase and tile c's preparation are done
-    // ------------------------------------------------------------ load phase
-    {
+    if (c + 1 < ntiles) {
+      // cumulative decay of tile c + 1 from the registers loaded in the phase before
       const int pn = (c + 1) & 1;
-      // P waves: raw q and k rows of tile c + 1 and v rows of tile c of their stream; rows >= sub
-      // are written as zeros (whole tiles take the branch without selects)
-      if (!isG) {
-        bf16* const qb = QB(gs, pn) + e0;
-        bf16* const kb = KB(gs, pn) + e0;
-        bf16* const vb = VB(gs) + e0;
-        if (a.sub == 32 && c >= 0 && c + 1 < ntiles) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int r = lr0 + 4 * i;
-            *(bf16x8*)(qb + r * QROW) = rq[i];
-            *(bf16x8*)(kb + r * QROW) = rk[i];
-            *(bf16x8*)(vb + r * QROW) = rv[i];
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int r = lr0 + 4 * i;
-            const bool real = r < a.sub;
-            if (c + 1 < ntiles) {
-              *(bf16x8*)(qb + r * QROW) = real ? rq[i] : vzero;
-              *(bf16x8*)(kb + r * QROW) = real ? rk[i] : vzero;
-            }
-            if (c >= 0) *(bf16x8*)(vb + r * QROW) = real ? rv[i] : vzero;
-          }
+      if (isG) {
+        const float gam = gamma_scan(rg, false);
+        const float gall = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gam), 31));
+        if (h == 0) {
+          float* va = VA(gs);
+          va[VA_GAML + l32] = gam * LOG2E;
+          va[VA_BET + l32] = l32 < a.sub ? rb : 0.f;
+          va[VA_EG + l32] = __builtin_amdgcn_exp2f(gam * LOG2E);
+          va[VA_EGL + l32] = __builtin_amdgcn_exp2f((gall - gam) * LOG2E);
+        }
+      } else {
+        const float gam = gamma_scan(rgp, false);
+        if (h == 0) {
+          float* vp = VP(gs);
+          vp[VP_GAML + l32] = gam * LOG2E;
+          vp[VP_EG + l32] = __builtin_amdgcn_exp2f(gam * LOG2E);
         }
       }
-      if (c + 1 < ntiles) {
-        // cumulative decay of the next tile: inclusive scan of g over its rows (lanes 0..31)
-        if (isG) {
-          const bool greal = h == 0 && l32 < a.sub;
-          float x = greal ? rg : 0.f;
-          x += dpp_mov<0x111>(x);  // row_shr:1
-          x += dpp_mov<0x112>(x);  // row_shr:2
-          x += dpp_mov<0x114>(x);  // row_shr:4
-          x += dpp_mov<0x118>(x);  // row_shr:8
-          x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
-          const float gam = x;
-          const float gall = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 31));
-          if (h == 0) {
-            float* va = VA(gs);
-            va[VA_GAML + l32] = gam * LOG2E;
-            va[VA_BET + l32] = greal ? rb : 0.f;
-            va[VA_EG + l32] = __builtin_amdgcn_exp2f(gam * LOG2E);
-            va[VA_EGL + l32] = __builtin_amdgcn_exp2f((gall - gam) * LOG2E);
-          }
-        }
-      }
+      wave_lds_sync();
+      (void)pn;
     }
-    __syncthreads();
-    issue_loads(c + 2 < ntiles ? c + 2 : -1, c + 1 < ntiles ? c + 1 : -1);
+    if (c + 1 < ntiles) issue_loads(c + 2 < ntiles ? c + 2 : -1, c + 1);
 
     // ------------------------------------------------------------ preparation of tile c + 1
     {
@@ -1111,7 +1126,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const bool in = 8 * m + 4 * ho + e <= lo;
-              tv1[4 * m + e] = in ? -(t4[e] * (be4[e] * eg4[e] * rk4[e])) : 0.f;  // -T1: W is stored negated
+              tv1[4 * m + e] = in ? -(t4[e] * (be4[e] * eg4[e] * rk4[e])) : 0.f;  // -T1
               tv2[4 * m + e] = in ? t4[e] * be4[e] : 0.f;
             }
           }
@@ -1121,20 +1136,10 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           bf16x8* t2d = T2f(gs, pn) + 2 * lane;
           t2d[0] = f2.lo;
           t2d[1] = f2.hi;
-          // W^T = K^T T1^T per 32-column slice of k with the permuted transposed read: lane = row
-          // l32 of W, value v = k column 32 kt + 16 h + v, stored as two 16-byte runs
-          bf16* const W = WB(gs, pn);
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt) {
-            F fb, fwo;
-            lds_frag_tr_d(K + kt * 32, QROW, lane, fb);
-            f32x16 aw = zero16();
-            mma32(aw, fb, f1);
-            acc_to_frag(aw, fwo);
-            bf16x8* const wr = (bf16x8*)(W + l32 * QROW + kt * 32 + 16 * h);
-            wr[0] = fwo.lo;
-            wr[1] = fwo.hi;
-          }
+          // -T1 as the A operand of V' = U - T1 (K S): the state waves apply it to their K S
+          bf16x8* t1d = T1f(gs, pn) + 2 * lane;
+          t1d[0] = f1.lo;
+          t1d[1] = f1.hi;
         } else {
           // P^T = K Q^T: lane = query row l32, values = key rows rho(v, h); P_ij = mask(scale/||q_i||
           // q_i . k^_j e^(gamma_i - gamma_j)), j <= i, with 1/||k_j|| applied to V' instead
@@ -1146,13 +1151,13 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
             lds_frag_c(K + l32 * QROW + kt * 32, h, fk[kt]);
           }
 #pragma unroll
-          for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(va + VA_GAML + 8 * m + 4 * h);
+          for (int m = 0; m < 4; ++m) gam4[m] = *(const f32x4*)(VP(gs) + VP_GAML + 8 * m + 4 * h);
           f32x16 acc = zero16();
 #pragma unroll
           for (int kt = 0; kt < KT; ++kt) mma32(acc, fk[kt], fq[kt]);
           __builtin_amdgcn_sched_group_barrier(0x100, 4 * KT + 4, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 2 * KT, 0);
-          const float gi = va[VA_GAML + l32];
+          const float gi = VP(gs)[VP_GAML + l32];
           // scale / ||q|| of query row l32 from this lane's half of the row and the other half's
           const float rqi = a.l2norm ? a.scale * rsqrtf(row_sumsq(fq) + 1e-6f) : a.scale;
           // P is kept as the A operand fragment of P V' (lane = query row, values = key rows in
@@ -1170,8 +1175,24 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           bf16x8* const pd = PBf(gs, pn) + 2 * lane;
           pd[0] = fpo.lo;
           pd[1] = fpo.hi;
-          if (h == 0) vs[VS_EGQ + l32] = va[VA_EG + l32] * rqi;
+          if (h == 0) vs[VS_EGQ + l32] = VP(gs)[VP_EG + l32] * rqi;
         }
+      }
+    }
+    if (!isG) {
+      // tile c + 1's v rows into the other v buffer; tile c + 2's q and k rows into tile c's
+      // buffers once every state wave has read them (the state waves raise `flag` by one each per
+      // tile; the wait is bounded, and they reach their raise without waiting on this wave)
+      if (c + 1 < ntiles) put_rows(VB(gs, (c + 1) & 1), rv);
+      if (c + 2 < ntiles) {
+        const unsigned target = 4u * (unsigned)(c + 1);
+        for (int spin = 0; spin < (1 << 22); ++spin) {
+          if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("" ::: "memory");
+        put_rows(QB(gs, c & 1), rq);
+        put_rows(KB(gs, c & 1), rk);
       }
     }
   }
@@ -1182,64 +1203,78 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   for (int t = 0; t < KT; ++t) S[t] = zero16();
   for (int c = -1; c < ntiles; ++c) {
     __syncthreads();  // tile c-1's state phase and tile c's preparation are done
-    __syncthreads();  // the load phase is done
     if (c >= 0) {
       // ---------------------------------------------------------- state phase, tile c
       const int pc = c & 1;
       const int t0 = c * a.sub;
-      // V' = U - W S accumulates in one tile per stream: U = T2 V first, then the products with
-      // the negated W rows the preparation stored
-      f32x16 accV[2], accQS[2];
+      // K S and Q S of both streams from the clean state before the tile; the K and Q fragments
+      // of slice kt + 1 are read while the products of slice kt run
+      f32x16 accKS[2], accQS[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        accV[s] = zero16();
+        accKS[s] = zero16();
         accQS[s] = zero16();
-        F ft, fv;
-        const bf16x8* t2 = T2f(s, pc) + 2 * lane;
-        ft.lo = t2[0];
-        ft.hi = t2[1];
-        lds_frag_tr(VB(s) + u * 32, QROW, lane, fv);
-        mma32(accV[s], ft, fv);  // U = T2 V
       }
-      // -W S and Q S of both streams from the clean state before the tile; the W and Q fragments
-      // of slice kt + 1 are read while the products of slice kt run
-      F fw[2][2], fq[2][2];  // [slice parity][stream]
-      auto read_wq = [&](int kt) {
+      F fk2[2][2], fq[2][2];  // [slice parity][stream]
+      auto read_kq = [&](int kt) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          lds_frag_c(WB(s, pc) + l32 * QROW + kt * 32, h, fw[kt & 1][s]);
+          lds_frag_c(KB(s, pc) + l32 * QROW + kt * 32, h, fk2[kt & 1][s]);
           lds_frag_c(QB(s, pc) + l32 * QROW + kt * 32, h, fq[kt & 1][s]);
         }
       };
-      read_wq(0);
+      read_kq(0);
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
         F sx;
         acc_to_frag(S[kt], sx);
-        if (kt + 1 < KT) read_wq(kt + 1);
+        if (kt + 1 < KT) read_kq(kt + 1);
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          mma32(accV[s], fw[kt & 1][s], sx);
+          mma32(accKS[s], fk2[kt & 1][s], sx);
           mma32(accQS[s], fq[kt & 1][s], sx);
         }
       }
-      // issue order: the U operand reads, slice 0's reads, the U products, then each slice's
-      // products behind the next slice's reads (keeps eight LDS reads in flight per wave)
-      __builtin_amdgcn_sched_group_barrier(0x100, 12, 1);
+      // issue order: slice 0's reads, then each slice's products behind the next slice's reads
+      // (keeps eight LDS reads in flight per wave)
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
 #pragma unroll
       for (int kt = 0; kt + 1 < KT; ++kt) {
         __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
         __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+      // the clean k rows as the A operand of the state update, read now: after them this wave has
+      // read every q and k row of tile c, and the P waves may overwrite those buffers
+      F fku[KT];
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) lds_frag_tr_d(KB(0, pc) + kt * 32, QROW, lane, fku[kt]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      // V' = U - T1 (K S) = T2 V + (-T1) (K S): W = T1 K is never formed; K S feeds straight back
+      // as the B operand of the -T1 product (its rows are the tile rows in rho order)
+      f32x16 accV[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        accV[s] = zero16();
+        F ft, fv, ft1, fks;
+        const bf16x8* t2 = T2f(s, pc) + 2 * lane;
+        ft.lo = t2[0];
+        ft.hi = t2[1];
+        const bf16x8* t1 = T1f(s, pc) + 2 * lane;
+        ft1.lo = t1[0];
+        ft1.hi = t1[1];
+        lds_frag_tr(VB(s, pc) + u * 32, QROW, lane, fv);
+        acc_to_frag(accKS[s], fks);
+        mma32(accV[s], ft, fv);    // U = T2 V
+        mma32(accV[s], ft1, fks);  // - T1 K S
+      }
       const int rs = opaque(a.Hv * a.Dv);  // token stride of the outputs
 #pragma unroll
       for (int si = 0; si < 2; ++si) {
         const int s = 1 - si;  // noised first: the clean update below overwrites S
         const float* vs = VS(s, pc);
-        // O = diag(e^gamma scale/||q||) Q S + P (V' / ||k||),  V' = U - W S
+        // O = diag(e^gamma scale/||q||) Q S + P (V' / ||k||),  V' = U - T1 K S
         f32x16 vn, vk;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -1287,9 +1322,6 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           }
           F fd;
           acc_to_frag(vd, fd);
-          F fk[KT];
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt) lds_frag_tr_d(KB(0, pc) + kt * 32, QROW, lane, fk[kt]);
           // accumulator row rho(v, h) of slice kt is state row 32 kt + 16 h + v
           float* const sb = a.states ? a.states + (((long long)b * ntiles + c) * a.Hv + hv) * (128LL * 128) + u * 32 +
                                            16 * h * 128 + l32
@@ -1298,7 +1330,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) S[kt][v] *= lam;
-            mma32(S[kt], fk[kt], fd);
+            mma32(S[kt], fku[kt], fd);
             if (sb) {
 #pragma unroll
               for (int v = 0; v < 16; ++v)

@@ -530,8 +530,7 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
       const long long off = (long long)((BC ? 0 : kh * L) + key) * (isv ? a.v_st : a.k_st) + chunk * 8;
       const bf16* src = (isv ? vbase : kbase) + off;
       unsigned char* dst = sb + (isv ? SM::TILE_BYTES : 0) + row0 * (2 * D);
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+      dma_load16(src, dst);
     }
   };
   // wait until tile n's loads (this wave's) have landed, given which later tiles were issued
@@ -572,6 +571,17 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
         kf.lo = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 8 * h));
         kf.hi = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 16 + 8 * h));
         mma32(st, kf, qf[s]);
+      }
+      // issue order: the K fragments of two slices ahead of their products (four LDS reads in
+      // flight per wave instead of two)
+      if constexpr (DT >= 3) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
+#pragma unroll
+        for (int s = 0; s + 2 < DT; ++s) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
       }
 #pragma unroll
       for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;

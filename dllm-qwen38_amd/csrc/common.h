@@ -119,6 +119,17 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// Direct global -> LDS load of 16 bytes per lane: lane i's 16 bytes land at lds_base + 16 i
+// (lds_base wave-uniform). Emitted as inline assembly: the compiler cannot tell a kernel's LDS
+// stage buffers apart, so for its own load-to-LDS builtin it waits for every such load in flight
+// before each later LDS read and at every barrier, which serialises a prefetch ring. Callers wait
+// for these loads with explicit vmcnt counts.
+__device__ __forceinline__ void dma_load16(const void* src, const void* lds_base) {
+  typedef const __attribute__((address_space(3))) void* lds_cptr;
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_cptr)lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
 // Ordering point for LDS traffic between lanes of ONE wavefront (no s_barrier): LDS operations of
 // a wave complete in issue order, so only compiler reordering has to be prevented.
 __device__ __forceinline__ void wave_lds_sync() {

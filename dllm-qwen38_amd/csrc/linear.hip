@@ -86,18 +86,14 @@ __global__ __launch_bounds__(256) void decode_linear_kernel(LinArgs a) {
       const int n = min(n0 + row, N - 1);  // rows past N load a valid row; their outputs are not stored
       const int c = schunk ^ ((row >> 1) & 7);
       const bf16* src = w + (long long)n * K + k0 + 8 * c;
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(sb + (32 * wave + 8 * i) * 128), 16,
-                                       0, 0);
+      dma_load16(src, sb + (32 * wave + 8 * i) * 128);
     }
     {  // token tile: wave w stages rows 8 w .. 8 w + 7
       const int row = 8 * wave + srow;
       const int m = min(m0 + row, M - 1);
       const int c = schunk ^ ((row >> 1) & 7);
       const bf16* src = x + (long long)m * K + k0 + 8 * c;
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(sb + LIN_W_BYTES + 8 * wave * 128), 16,
-                                       0, 0);
+      dma_load16(src, sb + LIN_W_BYTES + 8 * wave * 128);
     }
   };
   constexpr int PER = 5;  // direct loads per wave per step

@@ -3,32 +3,41 @@
 //
 // A cached denoising step runs every projection of the stack on one block of tokens (32 rows), so
 // each weight is read once for 32 rows and the step is bound by streaming the weights from HBM.
-// The weights stream through LDS in wide coalesced reads:
-//   * a workgroup owns 128 output features (four 32x32 accumulator tiles, one per wave) and a
-//     range of K. Per step of 64 k it stages the weight tile [128 features x 64 k] and the token
-//     tile [32 rows x 64 k] with direct global -> LDS loads (each wave instruction moves 1 KB: eight
+//   * Work units. An output tile is 128 features x 32 token rows; a unit is one step of 64 k of one
+//     tile (16 KB of weights). The launch has G workgroups, and workgroup w takes the contiguous
+//     unit range [w U / G, (w + 1) U / G) of the U units, in tile order. With fewer than two tiles
+//     per CU, G is one per CU: every CU streams the same number of bytes whatever the projection's
+//     shape (a grid of whole tiles or of K splits leaves CUs idle, or with twice the work of
+//     others, at N = 5120). With more tiles (lm_head), G is the tile count: nothing is split.
+//   * Per unit the workgroup stages the weight tile [128 features x 64 k] and the token tile
+//     [32 rows x 64 k] with direct global -> LDS loads (each wave instruction moves 1 KB: eight
 //     whole 128-byte row segments, no registers), in a ring of LIN_NST stages that keeps
-//     LIN_NST - 1 steps in flight;
+//     LIN_NST - 1 units in flight, across tile boundaries;
 //   * rows are 128 bytes with their 16-byte chunks XOR-swizzled by (row >> 1), so the operand reads
 //     (16 rows of one chunk per pass) touch every bank once;
 //   * wave w reads the B operand (lane = feature) of its 32 features and the A operand (lane =
-//     token) from LDS, 16 bytes each, and issues four v_mfma_f32_32x32x16_bf16 per step (lane
+//     token) from LDS, 16 bytes each, and issues four v_mfma_f32_32x32x16_bf16 per unit (lane
 //     (row, h) carries k = 16u + 8h + 0..7 in MFMA u for both operands);
-//   * with one K range the tile is rounded to bf16 and stored; with several, fp32 partials
-//     [S, M, N] go to a workspace and a second kernel sums them in split order (deterministic);
-//   * more than 32 token rows: grid.z takes the next 32 rows (the weights are streamed again);
+//   * a tile whose units all belong to one workgroup is rounded to bf16 and stored. A tile split
+//     between workgroups leaves an fp32 partial per piece (at most two per workgroup: its first
+//     and its last piece); a second kernel sums the pieces in workgroup order (deterministic) for
+//     the split tiles only;
+//   * more than 32 token rows: the next 32 rows are further tiles (the weights are streamed again);
 //   * up to four projections of the same x (q | k | v, the four mixer inputs, gate | up) share one
-//     launch and one split reduction: the grid's tiles run through the weights in turn. With the
-//     SwiGLU epilogue (gate | up) the reduction writes round(round(silu(gate)) * up), the MLP's
-//     activation, instead of the two projections.
+//     launch: the feature tiles run through the weights in turn. With the SwiGLU epilogue
+//     (gate | up) the second kernel writes round(round(silu(gate)) * up), the MLP's activation,
+//     over the whole gate projection (whole tiles were stored rounded, the up tiles in the
+//     workspace).
 #include "common.h"
 
 namespace dllm {
 
-constexpr int LIN_NST = 3;                 // ring stages
-constexpr int LIN_W_BYTES = 128 * 64 * 2;  // weight tile of one step
-constexpr int LIN_X_BYTES = 32 * 64 * 2;   // token tile of one step
+constexpr int LIN_NST = 4;                 // ring stages (4 x 20 KB: two workgroups fit a CU)
+constexpr int LIN_W_BYTES = 128 * 64 * 2;  // weight tile of one unit
+constexpr int LIN_X_BYTES = 32 * 64 * 2;   // token tile of one unit
 constexpr int LIN_STAGE = LIN_W_BYTES + LIN_X_BYTES;
+constexpr int LIN_TILE = 32 * 128;         // floats of one partial tile
+constexpr int LIN_CUS = 256;               // compute units of the chip (MI355X)
 
 __device__ __forceinline__ int lin_off(int row, int chunk) {  // byte offset of a 16-byte chunk of a 128-byte row
   return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
@@ -40,163 +49,257 @@ __device__ __forceinline__ void lin_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// wait until at most `behind` units of PER loads each are in flight (behind <= B)
+template <int B, int PER>
+__device__ __forceinline__ void lin_wait_behind(int behind) {
+  if constexpr (B > 0) {
+    if (behind >= B) lin_wait_vmcnt<B * PER>();
+    else lin_wait_behind<B - 1, PER>(behind);
+  } else {
+    lin_wait_vmcnt<0>();
+  }
+}
+
 constexpr int LIN_MAXSEG = 4;
 struct LinSeg {
   const bf16* w;  // [N, K]
   bf16* y;        // [M, N]
-  float* part;    // [S, M, N] fp32 partials (split path)
   int N;
-  int tile0;      // first grid tile of this projection
-  long long e0;   // first element of this projection in the reduction's index space
+  int tile0;      // first feature tile of this projection
 };
 struct LinArgs {
   const bf16* x;
   LinSeg seg[LIN_MAXSEG];
-  int nseg, M, K, kchunk, S, split_path, swiglu;
+  float* part;    // [G][2][32][128] fp32 partial tiles: a workgroup's first and last piece
+  bf16* up;       // swiglu: the up projection's whole tiles [M, N], rounded
+  int nseg, M, K;
+  int ntn;        // feature tiles over all projections
+  int ns;         // units per tile (K / 64)
+  int units;      // tiles * ns, tiles = ntn * ceil(M / 32)
+  int uq, ur;     // units = uq * G + ur
+  int G, swiglu;
 };
+
+// First unit of workgroup w, floor(w U / G) = w q + floor(w r / G) with U = q G + r (32-bit: w, r < G
+// <= 32768). The workgroup whose range holds unit u: floor(((u + 1) G - 1) / U), the largest w with
+// start(w) <= u; the quotient in double is exact here (numerator < 2^46, and a quotient just below
+// an integer k <= G is at least 1/U >= 2^-31 below it, far more than a double's spacing near k).
+__device__ __forceinline__ int lin_start(const LinArgs& a, int w) { return w * a.uq + (w * a.ur) / a.G; }
+__device__ __forceinline__ int lin_owner(const LinArgs& a, int u) {
+  return (int)(((double)(u + 1) * a.G - 1.0) / (double)a.units);
+}
+__device__ __forceinline__ int lin_seg(const LinArgs& a, int nt) {  // projection of feature tile nt
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < LIN_MAXSEG; ++i)
+    if (i < a.nseg && nt >= a.seg[i].tile0) si = i;
+  return si;
+}
 
 __global__ __launch_bounds__(256) void decode_linear_kernel(LinArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[LIN_NST * LIN_STAGE];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-  const int split = blockIdx.y, m0 = blockIdx.z * 32;
-  int si = 0;
-#pragma unroll
-  for (int i = 1; i < LIN_MAXSEG; ++i)
-    if (i < a.nseg && (int)blockIdx.x >= a.seg[i].tile0) si = i;
-  const LinSeg& sg = a.seg[si];
+  const int u0 = lin_start(a, blockIdx.x);
+  const int nunits = lin_start(a, blockIdx.x + 1) - u0;
   const bf16* __restrict__ const x = a.x;
-  const bf16* __restrict__ const w = sg.w;
-  const int M = a.M, N = sg.N, K = a.K, kchunk = a.kchunk;
-  const int tile = blockIdx.x - sg.tile0;
-  const int n0 = tile * 128;
-  const int kb = split * kchunk;
-  const int ke = min(K, kb + kchunk);
-  const int nsteps = ke > kb ? (ke - kb) / 64 : 0;  // K and kchunk are multiples of 64
+  const int M = a.M, K = a.K, ns = a.ns;
 
   // staging role of this lane: row 8 i + lane / 8 of its rows, logical chunk (lane % 8) ^ key(row)
   const int srow = lane >> 3, schunk = lane & 7;
-  auto stage = [&](int s) {
-    unsigned char* sb = smem + (s % LIN_NST) * LIN_STAGE;
-    const int k0 = kb + 64 * s;
+  int st_tile = u0 / ns, st_step = u0 - st_tile * ns;  // unit the next stage() call loads
+  auto stage = [&](int j) {  // unit u0 + j into ring slot j % LIN_NST
+    const int mt = st_tile / a.ntn, nt = st_tile - mt * a.ntn;
+    const LinSeg& sg = a.seg[lin_seg(a, nt)];
+    const int n0 = (nt - sg.tile0) * 128, m0 = mt * 32, k0 = 64 * st_step;
+    unsigned char* sb = smem + (j % LIN_NST) * LIN_STAGE;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {  // this wave's 4 of the 16 weight instructions: rows 32 wave + 8 i ..
       const int row = 32 * wave + 8 * i + srow;
-      const int n = min(n0 + row, N - 1);  // rows past N load a valid row; their outputs are not stored
+      const int n = min(n0 + row, sg.N - 1);  // rows past N load a valid row; their outputs are not stored
       const int c = schunk ^ ((row >> 1) & 7);
-      const bf16* src = w + (long long)n * K + k0 + 8 * c;
-      dma_load16(src, sb + (32 * wave + 8 * i) * 128);
+      dma_load16(sg.w + (long long)n * K + k0 + 8 * c, sb + (32 * wave + 8 * i) * 128);
     }
     {  // token tile: wave w stages rows 8 w .. 8 w + 7
       const int row = 8 * wave + srow;
       const int m = min(m0 + row, M - 1);
       const int c = schunk ^ ((row >> 1) & 7);
-      const bf16* src = x + (long long)m * K + k0 + 8 * c;
-      dma_load16(src, sb + LIN_W_BYTES + 8 * wave * 128);
+      dma_load16(x + (long long)m * K + k0 + 8 * c, sb + LIN_W_BYTES + 8 * wave * 128);
     }
+    if (++st_step == ns) st_step = 0, ++st_tile;
   };
-  constexpr int PER = 5;  // direct loads per wave per step
-  static_assert(LIN_NST == 3, "wait_step assumes at most one step in flight behind the waited one");
-  auto wait_step = [&](int s) {  // step s has landed for this wave (step s + 1 may still travel)
-    if (s + 1 < nsteps) lin_wait_vmcnt<PER>();
-    else lin_wait_vmcnt<0>();
+  constexpr int PER = 5;  // direct loads per wave per unit
+  static_assert(LIN_NST >= 2 && LIN_NST * LIN_STAGE <= 160 * 1024, "ring depth");
+  // unit j has landed for this wave; the units issued after it may still travel
+  auto wait_unit = [&](int j) { lin_wait_behind<LIN_NST - 2, PER>(min(LIN_NST - 2, nunits - 1 - j)); };
+
+  // acc: lane holds feature column l32 of this wave's 32 features, token rows rho(v, h)
+  auto flush = [&](int tile, bool whole, int slot, const f32x16& acc) {
+    const int mt = tile / a.ntn, nt = tile - mt * a.ntn;
+    const int si = lin_seg(a, nt);
+    const LinSeg& sg = a.seg[si];
+    if (whole) {
+      const int n = (nt - sg.tile0) * 128 + 32 * wave + l32;
+      bf16* const y = (a.swiglu && si == 1) ? a.up : sg.y;
+      if (n >= sg.N) return;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = mt * 32 + rho(v, h);
+        if (m < M) y[(long long)m * sg.N + n] = (bf16)acc[v];
+      }
+    } else {
+      float* const p = a.part + (long long)(2 * blockIdx.x + slot) * LIN_TILE + 32 * wave + l32;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) p[rho(v, h) * 128] = acc[v];
+    }
   };
 
   f32x16 acc = zero16();
 #pragma unroll
-  for (int s = 0; s < LIN_NST - 1; ++s)
-    if (s < nsteps) stage(s);
-  if (nsteps > 0) wait_step(0);
+  for (int j = 0; j < LIN_NST - 1; ++j)
+    if (j < nunits) stage(j);
+  if (nunits > 0) wait_unit(0);
   __syncthreads();
-  for (int s = 0; s < nsteps; ++s) {
-    if (s + LIN_NST - 1 < nsteps) stage(s + LIN_NST - 1);  // its stage held step s - 1, done before the barrier
-    const unsigned char* sb = smem + (s % LIN_NST) * LIN_STAGE;
+  int tile = u0 / ns, step = u0 - tile * ns;
+  int pstep0 = step, slot = 0;  // step the current piece began at; partial slot of the piece
+  for (int j = 0; j < nunits; ++j) {
+    if (j + LIN_NST - 1 < nunits) stage(j + LIN_NST - 1);  // its slot held unit j - 1, done before the barrier
+    const unsigned char* sb = smem + (j % LIN_NST) * LIN_STAGE;
     const unsigned char* xs = sb + LIN_W_BYTES;
-    bf16x8 a[4], bv[4];
+    bf16x8 av[4], bv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      a[u] = *(const bf16x8*)(xs + lin_off(l32, 2 * u + h));
+      av[u] = *(const bf16x8*)(xs + lin_off(l32, 2 * u + h));
       bv[u] = *(const bf16x8*)(sb + lin_off(32 * wave + l32, 2 * u + h));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[u], bv[u], acc, 0, 0, 0);
-    if (s + 1 < nsteps) wait_step(s + 1);
-    __syncthreads();  // step s + 1 staged by every wave; every wave is done with step s's stage
-  }
-  // acc: lane holds feature column l32 of this wave's tile, token rows rho(v, h)
-  const int n = n0 + 32 * wave + l32;
-  if (n >= N) return;
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int m = m0 + rho(v, h);
-    if (m >= M) continue;
-    if (a.split_path) sg.part[((long long)split * M + m) * N + n] = acc[v];
-    else sg.y[(long long)m * N + n] = (bf16)acc[v];
+    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[u], bv[u], acc, 0, 0, 0);
+    if (step == ns - 1 || j == nunits - 1) {  // the piece ends: the tile's last unit or the range's
+      flush(tile, pstep0 == 0 && step == ns - 1, slot, acc);
+      acc = zero16();
+      slot = 1;
+      pstep0 = 0;
+    }
+    if (++step == ns) step = 0, ++tile;
+    if (j + 1 < nunits) wait_unit(j + 1);
+    __syncthreads();  // unit j + 1 staged by every wave; every wave is done with unit j's stage
   }
 }
 
-// y = bf16(sum over splits of part[s]) in split order, for every projection of the launch; with
-// the SwiGLU epilogue (two projections of equal N) y0 = round(round(silu(gate)) * up) instead.
-__global__ __launch_bounds__(256) void decode_linear_reduce_kernel(LinArgs a, long long total) {
-  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (e >= total) return;
-  int si = 0;
+// Sum of a tile's pieces at elements 4 q .. 4 q + 3 (row q / 32, columns 4 (q % 32) ..) in
+// workgroup order: the pieces of its owners w0..w1. A piece is its workgroup's first (slot 0) unless
+// the workgroup began in an earlier tile, which only the first owner can have (then the piece is
+// its last, slot 1). The pieces' 16-byte loads go out eight at a time before their sums.
+__device__ __forceinline__ f32x4 lin_sum_pieces(const LinArgs& a, int t0, int w0, int w1, int q) {
+  const f32x4* const p = (const f32x4*)a.part + q;
+  constexpr int T4 = LIN_TILE / 4;
+  f32x4 s = p[(long long)(2 * w0 + (lin_start(a, w0) >= t0 ? 0 : 1)) * T4];
+  for (int wb = w0 + 1; wb <= w1; wb += 8) {
+    f32x4 v[8];
 #pragma unroll
-  for (int i = 1; i < LIN_MAXSEG; ++i)
-    if (i < a.nseg && e >= a.seg[i].e0) si = i;
-  const long long MN0 = (long long)a.M * a.seg[si].N;
-  const long long i = e - a.seg[si].e0;
-  const float* p = a.seg[si].part + i;
-  float s = p[0];
-  for (int j = 1; j < a.S; ++j) s += p[(long long)j * MN0];
-  if (!a.swiglu) {
-    a.seg[si].y[i] = (bf16)s;
-    return;
+    for (int i = 0; i < 8; ++i)
+      if (wb + i <= w1) v[i] = p[(long long)(2 * (wb + i)) * T4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (wb + i <= w1) s += v[i];
   }
-  const float* pu = a.seg[1].part + i;  // swiglu: index space is the gate's; up has the same shape
-  float su = pu[0];
-  for (int j = 1; j < a.S; ++j) su += pu[(long long)j * MN0];
-  const float g = round_through<bf16>(s), u = round_through<bf16>(su);
-  a.seg[0].y[i] = (bf16)(round_through<bf16>(silu_f32(g)) * u);
+  return s;
+}
+
+constexpr int LIN_FIXMAX = 512;
+struct LinFix {
+  int n;                   // split tiles in this launch
+  int tile[LIN_FIXMAX];
+};
+constexpr int LIN_FIX_CHUNKS = LIN_TILE / 4 / 256;  // blocks per tile: one float4 per thread
+
+// Tiles split between workgroups (listed by the host): block (i, c) sums chunk c of tile i's pieces.
+__global__ __launch_bounds__(256) void decode_linear_fixup_kernel(LinArgs a, LinFix f) {
+  const int tile = f.tile[blockIdx.x];
+  const int t0 = tile * a.ns, w0 = lin_owner(a, t0), w1 = lin_owner(a, t0 + a.ns - 1);
+  const int mt = tile / a.ntn, nt = tile - mt * a.ntn;
+  const LinSeg& sg = a.seg[lin_seg(a, nt)];
+  const int q = blockIdx.y * 256 + threadIdx.x;
+  const f32x4 s = lin_sum_pieces(a, t0, w0, w1, q);
+  const int m = mt * 32 + (q >> 5), n = (nt - sg.tile0) * 128 + 4 * (q & 31);
+  if (m >= a.M) return;
+  bf16* const y = sg.y + (long long)m * sg.N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (n + i < sg.N) y[n + i] = (bf16)s[i];
+}
+
+// SwiGLU epilogue over every gate tile, block (tile, c) for chunk c: y0 = round(round(silu(gate)) *
+// up), gate and up each the rounded sum of their tile (stored whole by the main kernel, or summed
+// here from the pieces).
+__global__ __launch_bounds__(256) void decode_linear_swiglu_kernel(LinArgs a) {
+  const int ntg = a.seg[1].tile0;  // gate tiles per 32 token rows
+  const int mt = blockIdx.x / ntg, ng = blockIdx.x - mt * ntg;
+  const int tg = mt * a.ntn + ng, tu = tg + ntg;
+  const int N = a.seg[0].N;
+  const int g0 = tg * a.ns, gw0 = lin_owner(a, g0), gw1 = lin_owner(a, g0 + a.ns - 1);
+  const int u0 = tu * a.ns, uw0 = lin_owner(a, u0), uw1 = lin_owner(a, u0 + a.ns - 1);
+  const int q = blockIdx.y * 256 + threadIdx.x;
+  const int m = mt * 32 + (q >> 5), n = ng * 128 + 4 * (q & 31);
+  if (m >= a.M) return;
+  f32x4 gs = {}, us = {};
+  if (gw0 != gw1) gs = lin_sum_pieces(a, g0, gw0, gw1, q);
+  if (uw0 != uw1) us = lin_sum_pieces(a, u0, uw0, uw1, q);
+  bf16* const y = a.seg[0].y + (long long)m * N;
+  const bf16* const up = a.up + (long long)m * N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (n + i >= N) break;
+    const float gv = gw0 == gw1 ? (float)y[n + i] : round_through<bf16>(gs[i]);
+    const float uv = uw0 == uw1 ? (float)up[n + i] : round_through<bf16>(us[i]);
+    y[n + i] = (bf16)(round_through<bf16>(silu_f32(gv)) * uv);
+  }
 }
 
 }  // namespace dllm
 
 using namespace dllm;
 
-extern "C" int dllm_decode_linear_splits(int M, int N, int K) {
-  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+static long long lin_units(int M, long long ntn, int K) { return ntn * ((M + 31) / 32) * (K / 64); }
+
+extern "C" int dllm_decode_linear_workgroups(int M, int N, int K) {
+  if (M <= 0 || M > 64 || N <= 0 || K <= 0 || K % 64) return 0;
   const long long tiles = (long long)((N + 127) / 128) * ((M + 31) / 32);
-  // about 1.5 workgroups per CU, each K range at least 256 deep and at most 8 splits
-  long long s = (384 + tiles - 1) / tiles;
-  long long smax = K / 256 > 0 ? K / 256 : 1;
-  if (smax > 8) smax = 8;
-  if (s > smax) s = smax;
-  if (s < 1) s = 1;
-  return (int)s;
+  const long long u = tiles * (K / 64);
+  if (u > 0x7fffffffLL) return 0;
+  // enough whole tiles to fill the chip twice over: one tile per workgroup, nothing split;
+  // otherwise one workgroup per CU, each an equal share of the units
+  if (tiles >= 2 * LIN_CUS) return (int)(tiles < 32768 ? tiles : 32768);
+  return (int)(u < LIN_CUS ? u : LIN_CUS);
+}
+
+extern "C" long long dllm_decode_linear_workspace_bytes(int M, int N_gate, int workgroups, int swiglu) {
+  if (M <= 0 || workgroups <= 0 || N_gate < 0) return -1;
+  long long b = (long long)workgroups * 2 * LIN_TILE * sizeof(float);
+  if (swiglu) b += ((long long)M * N_gate * 2 + 255) / 256 * 256;
+  return b;
 }
 
 extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const void* const* weights,
-                                            void* const* outs, const int* Ns, float* workspace, int splits, int swiglu,
-                                            int dtype, void* stream) {
+                                            void* const* outs, const int* Ns, void* workspace, int workgroups,
+                                            int swiglu, int dtype, void* stream) {
   if (!x || !weights || !outs || !Ns) return fail(DLLM_EINVAL, "decode linear: null pointer");
   if (count < 1 || count > LIN_MAXSEG) return fail(DLLM_EINVAL, "decode linear: %d projections (1..%d)", count, LIN_MAXSEG);
-  if (M <= 0 || K <= 0 || splits <= 0) return fail(DLLM_EINVAL, "decode linear: bad sizes M=%d K=%d", M, K);
+  if (M <= 0 || K <= 0 || workgroups <= 0) return fail(DLLM_EINVAL, "decode linear: bad sizes M=%d K=%d", M, K);
   if (dtype != DT_BF16) return fail(DLLM_EUNSUPPORTED, "decode linear: bf16 only");
   if (K % 64) return fail(DLLM_EUNSUPPORTED, "decode linear: K=%d is not a multiple of 64", K);
   if (M > 64) return fail(DLLM_EUNSUPPORTED, "decode linear: M=%d > 64 rows (use a library GEMM)", M);
   if ((uintptr_t)x & 15) return fail(DLLM_EINVAL, "decode linear: x must be 16-byte aligned");
   if (swiglu && (count != 2 || Ns[0] != Ns[1])) return fail(DLLM_EINVAL, "decode linear: swiglu takes gate | up of equal N");
+  if (!workspace || ((uintptr_t)workspace & 15)) return fail(DLLM_EINVAL, "decode linear: the workspace must be a 16-byte aligned buffer");
   LinArgs a = {};
   a.x = (const bf16*)x;
   a.nseg = count;
   a.M = M; a.K = K;
-  a.kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;  // K range per split: whole 64-k steps
-  a.S = (K + a.kchunk - 1) / a.kchunk;
+  a.ns = K / 64;
   a.swiglu = swiglu;
-  a.split_path = a.S > 1 || swiglu;
-  long long tiles = 0, elems = 0;
+  long long ntn = 0;
   for (int i = 0; i < count; ++i) {
     if (!weights[i] || !outs[i] || Ns[i] <= 0) return fail(DLLM_EINVAL, "decode linear: projection %d is empty", i);
     if ((uintptr_t)weights[i] & 15) return fail(DLLM_EINVAL, "decode linear: weights must be 16-byte aligned");
@@ -204,31 +307,50 @@ extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int cou
     sg.w = (const bf16*)weights[i];
     sg.y = (bf16*)outs[i];
     sg.N = Ns[i];
-    sg.tile0 = (int)tiles;
-    sg.e0 = elems;
-    sg.part = a.split_path ? workspace + (long long)a.S * elems : nullptr;
-    tiles += (Ns[i] + 127) / 128;
-    elems += (long long)M * Ns[i];
+    sg.tile0 = (int)ntn;
+    ntn += (Ns[i] + 127) / 128;
   }
-  if (a.split_path && !workspace) return fail(DLLM_EINVAL, "decode linear: the split path needs a workspace");
-  if (tiles > 0x7fffffffLL) return fail(DLLM_EUNSUPPORTED, "decode linear: grid too large");
+  const long long units = lin_units(M, ntn, K);
+  if (units > 0x7fffffffLL) return fail(DLLM_EUNSUPPORTED, "decode linear: %lld work units is too many", units);
+  a.ntn = (int)ntn;
+  a.units = (int)units;
+  a.G = workgroups < units ? workgroups : (int)units;  // no workgroup without units
+  if (a.G > 32768) return fail(DLLM_EINVAL, "decode linear: %d workgroups (at most 32768)", workgroups);
+  a.uq = a.units / a.G;
+  a.ur = a.units % a.G;
+  a.part = (float*)workspace;
+  a.up = swiglu ? (bf16*)((char*)workspace + (long long)a.G * 2 * LIN_TILE * sizeof(float)) : nullptr;
   hipStream_t st = (hipStream_t)stream;
-  decode_linear_kernel<<<dim3((unsigned)tiles, a.S, (M + 31) / 32), 256, 0, st>>>(a);
+  decode_linear_kernel<<<dim3((unsigned)a.G), 256, 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear launch: %s", hipGetErrorString(e));
-  if (a.split_path) {
-    const long long total = swiglu ? (long long)M * Ns[0] : elems;
-    decode_linear_reduce_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, st>>>(a, total);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear reduce launch: %s", hipGetErrorString(e));
+  if (swiglu) {
+    decode_linear_swiglu_kernel<<<dim3((unsigned)(a.seg[1].tile0 * ((M + 31) / 32)), LIN_FIX_CHUNKS), 256, 0, st>>>(a);
+  } else {
+    // the tiles a range boundary falls inside, in batches of LIN_FIXMAX
+    LinFix f;
+    f.n = 0;
+    for (int b = 1; b <= a.G; ++b) {
+      const int ub = b < a.G ? (int)((long long)b * a.units / a.G) : -1;
+      const bool split = b < a.G && ub % a.ns != 0;
+      if (split && (f.n == 0 || f.tile[f.n - 1] != ub / a.ns)) f.tile[f.n++] = ub / a.ns;
+      if (f.n == LIN_FIXMAX || (b == a.G && f.n > 0)) {
+        decode_linear_fixup_kernel<<<dim3((unsigned)f.n, LIN_FIX_CHUNKS), 256, 0, st>>>(a, f);
+        e = hipGetLastError();
+        if (e != hipSuccess) break;
+        f.n = 0;
+      }
+    }
   }
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear fixup launch: %s", hipGetErrorString(e));
   return DLLM_OK;
 }
 
-extern "C" int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, float* workspace, int M, int N, int K,
-                                      int splits, int dtype, void* stream) {
+extern "C" int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, void* workspace, int M, int N, int K,
+                                      int workgroups, int dtype, void* stream) {
   const void* w[1] = {weight};
   void* o[1] = {y};
   const int n[1] = {N};
-  return dllm_decode_linear_multi_fwd(x, M, K, 1, w, o, n, workspace, splits, 0, dtype, stream);
+  return dllm_decode_linear_multi_fwd(x, M, K, 1, w, o, n, workspace, workgroups, 0, dtype, stream);
 }

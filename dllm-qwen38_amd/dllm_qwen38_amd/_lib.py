@@ -55,7 +55,8 @@ _SIGNATURES = {
     "dllm_bd_attention_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p]),
-    "dllm_decode_linear_splits": (_c_int, [_c_int, _c_int, _c_int]),
+    "dllm_decode_linear_workgroups": (_c_int, [_c_int, _c_int, _c_int]),
+    "dllm_decode_linear_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int]),
     "dllm_decode_linear_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_void_p]),
     "dllm_decode_linear_multi_fwd": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_voidpp, _c_voidpp, _c_intp,

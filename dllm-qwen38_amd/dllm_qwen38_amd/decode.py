@@ -109,10 +109,19 @@ def generate(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int, block
     return trace
 
 
+def _workspace(L, M: int, n_gate: int, G: int, swiglu: bool, dev) -> torch.Tensor:
+    """Workspace of one decoding-step projection launch: the fp32 pieces of the tiles split between
+    workgroups (and with swiglu the up projection's rounded tiles)."""
+    nbytes = L.dllm_decode_linear_workspace_bytes(M, n_gate, G, int(swiglu))
+    if nbytes <= 0:
+        raise ValueError(f"decode linear: no workspace size for M={M} workgroups={G}")
+    return torch.empty(-(-nbytes // 16) * 4, dtype=torch.float32, device=dev)
+
+
 def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
     """x [..., K] @ weight[N, K]^T for the few token rows of a decoding step (bf16, at most 64 rows,
-    K a multiple of 64) on the HIP kernel that streams the weight into MFMA operands; fp32
-    accumulation, deterministic. Returns [..., N] bf16."""
+    K a multiple of 64) on the HIP kernel that streams the weight into MFMA operands, every CU an
+    equal share of it; fp32 accumulation, deterministic. Returns [..., N] bf16."""
     dev = _lib.require_device(x, weight)
     K = x.shape[-1]
     N = weight.shape[0]
@@ -124,14 +133,14 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | 
     w = weight.contiguous()
     M = x2.shape[0]
     L = _lib.lib()
-    splits = L.dllm_decode_linear_splits(M, N, K)
-    if splits <= 0 or M > 64:
+    G = L.dllm_decode_linear_workgroups(M, N, K)
+    if G <= 0:
         raise ValueError(f"decode_linear does not take M={M} N={N} K={K} (M <= 64, K % 64 == 0)")
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev) if out is None else out
     if tuple(y.shape) != (M, N) or not y.is_contiguous() or y.dtype != torch.bfloat16:
         raise ValueError("out must be a contiguous bf16 [M, N] tensor")
-    ws = torch.empty(splits * M * N, dtype=torch.float32, device=dev) if splits > 1 else None
-    _lib.check(L.dllm_decode_linear_fwd(x2.data_ptr(), w.data_ptr(), y.data_ptr(), _lib.ptr(ws), M, N, K, splits,
+    ws = _workspace(L, M, 0, G, False, dev)
+    _lib.check(L.dllm_decode_linear_fwd(x2.data_ptr(), w.data_ptr(), y.data_ptr(), ws.data_ptr(), M, N, K, G,
                                         _lib.dtype_code(x.dtype), _lib.stream_handle(dev)), "dllm_decode_linear_fwd")
     return y.reshape(*x.shape[:-1], N)
 
@@ -153,18 +162,18 @@ def decode_linear_multi(x: torch.Tensor, weights: list, *, swiglu: bool = False)
     if swiglu and (len(ws) != 2 or Ns[0] != Ns[1]):
         raise ValueError("swiglu takes (gate, up) of equal N")
     L = _lib.lib()
-    splits = L.dllm_decode_linear_splits(M, sum(-(-n // 128) * 128 for n in Ns), K)
-    if splits <= 0 or M > 64:
+    G = L.dllm_decode_linear_workgroups(M, sum(-(-n // 128) * 128 for n in Ns), K)
+    if G <= 0:
         raise ValueError(f"decode_linear_multi does not take M={M} K={K} (M <= 64, K % 64 == 0)")
     outs = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in (Ns[:1] if swiglu else Ns)]
     if swiglu:
         outs.append(outs[0])  # not written
-    work = (torch.empty(splits * M * sum(Ns), dtype=torch.float32, device=dev) if splits > 1 or swiglu else None)
+    work = _workspace(L, M, Ns[0], G, swiglu, dev)
     n = len(ws)
     warr = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
     oarr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     narr = (ctypes.c_int * n)(*Ns)
-    _lib.check(L.dllm_decode_linear_multi_fwd(x2.data_ptr(), M, K, n, warr, oarr, narr, _lib.ptr(work), splits,
+    _lib.check(L.dllm_decode_linear_multi_fwd(x2.data_ptr(), M, K, n, warr, oarr, narr, work.data_ptr(), G,
                                               int(swiglu), _lib.dtype_code(x.dtype), _lib.stream_handle(dev)),
                "dllm_decode_linear_multi_fwd")
     lead = x.shape[:-1]

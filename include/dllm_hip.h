@@ -149,24 +149,28 @@ int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, con
  * contiguous. Replaces the nn.Linear calls (in_proj_*, q/k/v/o_proj, the MLP, lm_head) that every
  * denoising step of the reference decoder runs inside block_diffusion_forward
  * (src/dllm_qwen38/decode.py:63-66; [hf]:168-184,656-717) when they see one block of tokens.
- * splits > 1 splits K over workgroups; then workspace holds splits*M*N floats and a second launch
- * sums the splits in order (deterministic). dllm_decode_linear_splits(M, N, K) gives the split count
- * that fills the chip (0 if the shape is not taken).
+ * The launch has `workgroups` workgroups (at most 32768), each streaming an equal share of the
+ * (128-feature x 32-row tile, 64-k step) units; dllm_decode_linear_workgroups(M, N, K) gives one per
+ * CU, or one per tile when there are at least two tiles per CU (0 if the shape is not taken). Tiles
+ * split between workgroups leave fp32 pieces in `workspace` (dllm_decode_linear_workspace_bytes
+ * bytes, 16-byte aligned), which a second launch sums in workgroup order: deterministic for a given
+ * workgroup count.
  */
-int dllm_decode_linear_splits(int M, int N, int K);
-int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, float* workspace, int M, int N, int K,
-                           int splits, int dtype, void* stream);
+int dllm_decode_linear_workgroups(int M, int N, int K);
+long long dllm_decode_linear_workspace_bytes(int M, int N_gate, int workgroups, int swiglu);
+int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, void* workspace, int M, int N, int K,
+                           int workgroups, int dtype, void* stream);
 
 /*
  * Up to four projections of the same x in one launch (q | k | v; in_proj_qkv | z | b | a; gate |
- * up): weights[i] [Ns[i], K] -> outs[i] [M, Ns[i]], one split count for all (splits from
- * dllm_decode_linear_splits(M, sum of Ns rounded up to 128, K)). workspace holds
- * splits * M * sum(Ns) floats when splits > 1 or swiglu. swiglu = 1 (two projections gate | up
- * of equal N): outs[0] receives round(round(silu(gate)) * up), the MLP activation of
- * [hf]:704-717, and outs[1] is not written.
+ * up): weights[i] [Ns[i], K] -> outs[i] [M, Ns[i]], one workgroup count for all (from
+ * dllm_decode_linear_workgroups(M, sum of Ns rounded up to 128, K)); workspace of
+ * dllm_decode_linear_workspace_bytes(M, Ns[0], workgroups, swiglu) bytes. swiglu = 1 (two
+ * projections gate | up of equal N): outs[0] receives round(round(silu(gate)) * up), the MLP
+ * activation of [hf]:704-717, and outs[1] is not written.
  */
 int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const void* const* weights, void* const* outs,
-                                 const int* Ns, float* workspace, int splits, int swiglu, int dtype, void* stream);
+                                 const int* Ns, void* workspace, int workgroups, int swiglu, int dtype, void* stream);
 
 /*
  * Qwen3.5 RMSNorm over the last dim of x [rows, dim]: y = x * rsqrt(mean(x^2) + eps) * (1 + w)

@@ -61,15 +61,19 @@ def test_trace_tokens_per_forward():
     assert t.tokens_per_forward == 2.5 and decode.DecodeTrace(tokens=[]).tokens_per_forward == 0.0
 
 
-def test_decode_linear_split_rule_and_host_errors():
+def test_decode_linear_workgroup_rule_and_host_errors():
     from dllm_qwen38_amd import _lib
 
     L = _lib.lib()
-    assert L.dllm_decode_linear_splits(32, 100, 100) == 0  # K not a multiple of 64
-    assert L.dllm_decode_linear_splits(32, 151936, 5120) == 1  # 1187 feature tiles fill the chip alone
-    s = L.dllm_decode_linear_splits(32, 5120, 5120)
-    assert 1 < s <= 8
-    assert L.dllm_decode_linear_splits(32, 48, 5120) == 8
-    assert L.dllm_decode_linear_splits(32, 151936, 5120) == 1
+    assert L.dllm_decode_linear_workgroups(32, 100, 100) == 0  # K not a multiple of 64
+    assert L.dllm_decode_linear_workgroups(65, 100, 128) == 0  # more than 64 token rows
+    assert L.dllm_decode_linear_workgroups(32, 151936, 5120) == 1187  # >= 512 tiles: one per workgroup
+    assert L.dllm_decode_linear_workgroups(32, 5120, 5120) == 256  # one per CU, 15 units each
+    assert L.dllm_decode_linear_workgroups(1, 100, 64) == 1  # one unit: one workgroup
+    assert L.dllm_decode_linear_workgroups(33, 300, 320) == 3 * 2 * 5  # fewer units than CUs
+    # pieces: two fp32 [32, 128] tiles per workgroup; swiglu adds the up projection's bf16 rows
+    assert L.dllm_decode_linear_workspace_bytes(32, 0, 512, 0) == 512 * 2 * 32 * 128 * 4
+    assert L.dllm_decode_linear_workspace_bytes(32, 17408, 512, 1) == 512 * 2 * 32 * 128 * 4 + 32 * 17408 * 2
+    assert L.dllm_decode_linear_workspace_bytes(0, 0, 512, 0) == -1
     with pytest.raises(RuntimeError):
         decode.decode_linear(torch.zeros(32, 64, dtype=torch.bfloat16), torch.zeros(8, 64, dtype=torch.bfloat16))

@@ -13,6 +13,7 @@ Bars:
     2^-5 * max|logits| + 2^-6 * |logit| (bf16 activations, different GEMM shapes on each side).
 """
 
+import ctypes
 import copy
 
 import pytest
@@ -110,11 +111,80 @@ def test_decode_linear_matches_fp32_reference(dev, M, N, K):
     ref = x.float() @ w.float().T
     scale = x.float().abs() @ w.float().abs().T
     err = (got.float().cpu() - ref).abs()
-    print(f"M{M} N{N} K{K} splits {decode._lib.lib().dllm_decode_linear_splits(M, N, K)}: max|d|={err.max():.3e}")
+    print(f"M{M} N{N} K{K} workgroups {decode._lib.lib().dllm_decode_linear_workgroups(M, N, K)}: max|d|={err.max():.3e}")
     assert (err <= 2 ** -8 * ref.abs() + 2 ** -16 * scale).all()
     again = decode.decode_linear(x.to(dev), w.to(dev))
     torch.cuda.synchronize()
-    assert torch.equal(got, again), "split-K sums must be deterministic"
+    assert torch.equal(got, again), "the sums of split tiles must be deterministic"
+
+
+@pytest.mark.parametrize("G", [1, 2, 3, 7, 100, 191, 512])
+@pytest.mark.parametrize("swiglu", [0, 1])
+def test_decode_linear_any_workgroup_count(dev, G, swiglu):
+    """Every split of the (tile, k step) units over workgroups (2 row tiles x 6 feature tiles x 16
+    steps = 192 units; 512 asks for more workgroups than units and gets one unit each) gives the
+    projections within the bound of the single-launch test, and the same bits on a repeat."""
+    from dllm_qwen38_amd import _lib
+
+    g = torch.Generator().manual_seed(G + 10 * swiglu)
+    M, K, N = 40, 1024, 300
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    ws = [(torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16) for _ in range(2)]
+    L = _lib.lib()
+    xd, wd = x.to(dev), [w.to(dev) for w in ws]
+    outs = [torch.empty(M, N, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+
+    def run():
+        work = decode._workspace(L, M, N, G, bool(swiglu), dev)
+        warr = (ctypes.c_void_p * 2)(*[w.data_ptr() for w in wd])
+        oarr = (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs])
+        narr = (ctypes.c_int * 2)(N, N)
+        _lib.check(L.dllm_decode_linear_multi_fwd(xd.data_ptr(), M, K, 2, warr, oarr, narr, work.data_ptr(), G, swiglu,
+                                                  _lib.DT_BF16, _lib.stream_handle(dev)), "multi")
+        torch.cuda.synchronize()
+        return [o.clone().cpu() for o in outs]
+
+    got = run()
+    refs = [x.float() @ w.float().T for w in ws]
+    if swiglu:
+        gr, ur = (r.to(torch.bfloat16).float() for r in refs)
+        ref = torch.nn.functional.silu(gr).to(torch.bfloat16).float() * ur
+        err = (got[0].float() - ref).abs()
+        assert (err <= 2 ** -6 * ref.abs() + 2 ** -10 * ref.abs().max()).all()
+    else:
+        for o, w, ref in zip(got, ws, refs):
+            err = (o.float() - ref).abs()
+            assert (err <= 2 ** -8 * ref.abs() + 2 ** -16 * (x.float().abs() @ w.float().abs().T)).all()
+    again = run()
+    assert all(torch.equal(a, b) for a, b in zip(got[: 2 - swiglu], again[: 2 - swiglu]))
+
+
+def test_decode_linear_more_split_tiles_than_one_fixup_launch(dev):
+    """1199 workgroups over 600 tiles of 2 steps (1200 units): 599 tiles are split, more than the 512
+    one fixup launch lists, so the fixups go out in two launches; the result stays within the
+    single-launch bound and equals a repeat bit for bit."""
+    from dllm_qwen38_amd import _lib
+
+    g = torch.Generator().manual_seed(1199)
+    M, K, N, G = 32, 128, 128 * 600, 1199
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    L = _lib.lib()
+    xd, wd = x.to(dev), w.to(dev)
+
+    def run():
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        work = decode._workspace(L, M, 0, G, False, dev)
+        _lib.check(L.dllm_decode_linear_fwd(xd.data_ptr(), wd.data_ptr(), y.data_ptr(), work.data_ptr(), M, N, K, G,
+                                            _lib.DT_BF16, _lib.stream_handle(dev)), "decode linear")
+        torch.cuda.synchronize()
+        return y.cpu()
+
+    got = run()
+    ref = x.float() @ w.float().T
+    err = (got.float() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 2 ** -16 * (x.float().abs() @ w.float().abs().T)).all()
+    assert torch.equal(got, run())
 
 
 def test_decode_linear_multi_and_swiglu_epilogue(dev):

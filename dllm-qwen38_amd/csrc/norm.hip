@@ -83,6 +83,59 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x, c
   }
 }
 
+// The same for few rows: one workgroup of nw = blockDim.x / 64 waves per row, so that the rows of a
+// decoding step (32) spread over 32 CUs instead of 8, with the weights loaded beside the row (before
+// the reduction). dim == nw * 512 * NV; lane vectors (k nw + wave) * 64 + lane, 16 bytes each; the
+// sum of squares adds the waves' sums in wave order.
+template <typename T, typename TW, int NV>
+__global__ __launch_bounds__(512) void rmsnorm_row_kernel(const T* __restrict__ x, const T* __restrict__ r,
+                                                          T* __restrict__ sum_out, const TW* __restrict__ w,
+                                                          T* __restrict__ y, int dim, float eps, int unit) {
+  __shared__ float part[8];
+  const int nw = blockDim.x >> 6, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long long base = (long long)blockIdx.x * dim;
+  typedef __attribute__((ext_vector_type(8))) T V8;
+  typedef __attribute__((ext_vector_type(8))) TW W8;
+  float v[NV][8];
+  W8 wt[NV];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c0 = ((k * nw + wv) * 64 + lane) * 8;
+    const V8 xv = *(const V8*)(x + base + c0);
+    wt[k] = *(const W8*)(w + c0);
+    V8 sv = xv;
+    if (r) {
+      const V8 rv = *(const V8*)(r + base + c0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = from_f32<T>(to_f32(xv[i]) + to_f32(rv[i]));
+      if (sum_out) *(V8*)(sum_out + base + c0) = sv;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[k][i] = to_f32(sv[i]);
+      ss = __builtin_fmaf(v[k][i], v[k][i], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) part[wv] = ss;
+  __syncthreads();
+  float tot = part[0];
+  for (int i = 1; i < nw; ++i) tot += part[i];
+  const float inv = rsqrtf(tot / (float)dim + eps);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c0 = ((k * nw + wv) * 64 + lane) * 8;
+    V8 yv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float wf = to_f32(wt[k][i]);
+      yv[i] = from_f32<T>(v[k][i] * inv * (unit ? 1.f + wf : wf));
+    }
+    *(V8*)(y + base + c0) = yv;
+  }
+}
+
 // y = (w * round_T(rmsnorm(x))) * silu(z), the product rounded to T at each step as in the module
 template <typename T, typename TW>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict__ x, const T* __restrict__ z,
@@ -213,8 +266,26 @@ using namespace dllm;
 template <typename T, typename TW>
 static int launch_rmsnorm(const void* x, const void* r, void* so, const void* w, void* y, int rows, int dim, float eps,
                           int unit, bool vec, hipStream_t st) {
-  const dim3 grid((rows + 3) / 4), block(256);
   const int nv = vec && dim % 512 == 0 && dim / 512 <= 16 ? dim / 512 : 0;
+  if (nv > 1 && rows <= 256) {
+    // few rows (a decoding step): one workgroup of up to 8 waves per row
+    int nw = 8;
+    while (nv % nw) --nw;
+    const int nvw = nv / nw;
+    switch (nvw) {
+#define DLLM_RMS_ROW_CASE(N) \
+  case N: rmsnorm_row_kernel<T, TW, N><<<dim3(rows), dim3(64 * nw), 0, st>>>((const T*)x, (const T*)r, (T*)so, (const TW*)w, (T*)y, dim, eps, unit); break;
+      DLLM_RMS_ROW_CASE(1) DLLM_RMS_ROW_CASE(2) DLLM_RMS_ROW_CASE(3) DLLM_RMS_ROW_CASE(4) DLLM_RMS_ROW_CASE(5)
+      DLLM_RMS_ROW_CASE(6) DLLM_RMS_ROW_CASE(7) DLLM_RMS_ROW_CASE(8)
+#undef DLLM_RMS_ROW_CASE
+      default: break;
+    }
+    if (nvw <= 8) {
+      hipError_t e = hipGetLastError();
+      return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "rmsnorm launch: %s", hipGetErrorString(e));
+    }
+  }
+  const dim3 grid((rows + 3) / 4), block(256);
   switch (nv) {
 #define DLLM_RMS_CASE(N) \
   case N: rmsnorm_kernel<T, TW, N><<<grid, block, 0, st>>>((const T*)x, (const T*)r, (T*)so, (const TW*)w, (T*)y, rows, dim, eps, unit); break;

@@ -27,7 +27,7 @@ def _close(got, ref, dtype, name, floor=2 ** -12):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows,dim", [(37, 64), (64, 5120), (5, 1000)])
+@pytest.mark.parametrize("rows,dim", [(37, 64), (64, 5120), (5, 1000), (32, 2048), (8, 8192), (300, 5120)])
 def test_rmsnorm_with_and_without_residual(dev, dtype, rows, dim):
     g = torch.Generator().manual_seed(rows + dim)
     x = torch.randn(rows, dim, generator=g).to(dtype)

@@ -1383,7 +1383,11 @@ static int dispatch_gdn(GdnArgs& a, int dtype, bool fork, hipStream_t st) {
   const int dk = a.Dk <= 64 ? 64 : 128;
   if (dtype == DT_BF16) {
     if (dk == 64) return fork ? launch_gdn<64, 128, true, true>(a, st) : launch_gdn<64, 128, true, false>(a, st);
-    return fork ? launch_gdn<128, 128, true, true>(a, st) : launch_gdn<128, 128, true, false>(a, st);
+    if (fork) return launch_gdn<128, 128, true, true>(a, st);
+    // few (sequence, head) pairs (a decoding step: B = 1): two 64-column windows per head, so that
+    // twice the workgroups share the state loads (the columns are independent)
+    if ((long long)a.B * a.Hv < 128) return launch_gdn<128, 64, true, false>(a, st);
+    return launch_gdn<128, 128, true, false>(a, st);
   }
   if (dtype == DT_F32) {
     if (dk == 64) return fork ? launch_gdn<64, 64, false, true>(a, st) : launch_gdn<64, 64, false, false>(a, st);

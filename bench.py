@@ -93,10 +93,12 @@ def main(argv=None):
         return 2
     if a.workload == "attention":
         return bench_attention(a)
-    if a.workload == "stack":
-        return bench_stack(a)
-    if a.workload == "decode":
-        return bench_decode(a)
+    if a.workload in ("stack", "decode"):
+        # the library GEMMs around the path use the committed TunableOp solution table
+        from dllm_qwen38_amd import gemm_tuning
+
+        a.gemm_table = gemm_tuning.enable()
+        return bench_stack(a) if a.workload == "stack" else bench_decode(a)
 
     import torch
 
@@ -310,7 +312,7 @@ def bench_stack(a):
         "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": tf / BF16_MFMA_PEAK_TFLOPS, "traffic": None},
         "algorithmic_tflop": fl / 1e12, "params": hybrid.param_count(model) + lm_head.weight.numel(),
-        "wall_s_timed": wall, "cpu_baseline": None,
+        "gemm_table": getattr(a, "gemm_table", False), "wall_s_timed": wall, "cpu_baseline": None,
     }
     print(json.dumps(res))
     return 0
@@ -386,7 +388,8 @@ def bench_decode(a):
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None},
         "algorithmic_bytes": total, "weight_bytes": wbytes, "kv_cache_bytes": kv, "state_bytes": st,
         "prefill_ms": prefill_ms, "golden_step_ms": golden_ms, "speedup_vs_golden_step": golden_ms / ms,
-        "cache_bytes": cache.nbytes(), "wall_s_timed": wall, "cpu_baseline": None,
+        "cache_bytes": cache.nbytes(), "gemm_table": getattr(a, "gemm_table", False), "wall_s_timed": wall,
+        "cpu_baseline": None,
     }
     print(json.dumps(res))
     return 0

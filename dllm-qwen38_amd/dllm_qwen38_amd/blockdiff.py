@@ -90,16 +90,17 @@ def rotary_tables(text_model, L: int, device, dtype):
     return (emb.cos() * scale).to(dtype), (emb.sin() * scale).to(dtype)
 
 
-def _gdn_fork_arm(m, n0: torch.Tensor, nt: torch.Tensor, block: int, fault: BreakMode):
-    """LINEAR arm of the layer (blockdiff.py:153-177): both streams through one fused fork op."""
-    B, L, _ = n0.shape
+def _gdn_fork_arm(m, n: torch.Tensor, block: int, fault: BreakMode) -> torch.Tensor:
+    """LINEAR arm of the layer (blockdiff.py:153-177): both streams through one fused fork op.
+    n: [2B, L, D], rows 0..B-1 the noised stream, B..2B-1 the clean one; returns the same layout."""
+    B2, L, _ = n.shape
+    B = B2 // 2
     if fault.concat_causal_gdn:
-        out, _, _ = gdn.gdn_mixer_forward(m, torch.cat([nt, n0], 1), chunk_size=block, need_states=False)
-        return out[:, L:], out[:, :L]
-    x = torch.cat([nt, n0], 0)  # [2B, L, D]: rows 0..B-1 noised, B..2B-1 clean
-    raw = m.in_proj_qkv(x)
-    z = m.in_proj_z(x)
-    beta, g = gdn._beta_g(m, m.in_proj_b(x), m.in_proj_a(x))
+        out, _, _ = gdn.gdn_mixer_forward(m, torch.cat([n[:B], n[B:]], 1), chunk_size=block, need_states=False)
+        return torch.cat([out[:, :L], out[:, L:]], 0)
+    raw = m.in_proj_qkv(n)
+    z = m.in_proj_z(n)
+    beta, g = gdn._beta_g(m, m.in_proj_b(n), m.in_proj_a(n))
     Hv, Dv = m.num_v_heads, m.head_v_dim
     core = torch.empty(2 * B, L, Hv, Dv, dtype=raw.dtype, device=raw.device)
     gdn.gdn_state_fork(raw[B:], raw[:B], m.conv1d.weight.squeeze(1), beta[B:], beta[:B], g[B:], g[:B],
@@ -108,15 +109,16 @@ def _gdn_fork_arm(m, n0: torch.Tensor, nt: torch.Tensor, block: int, fault: Brea
                        fault="no-conv-prefix" if fault.drop_conv_prefix else None,
                        out={"ot": core[:B], "o0": core[B:]})
     o = norms.gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm.weight, _eps(m.norm)).reshape(2 * B, L, -1)
-    out = m.out_proj(o)
-    return out[B:], out[:B]
+    return m.out_proj(o)
 
 
-def _attention_arm(att, n0: torch.Tensor, nt: torch.Tensor, cos, sin, block: int, fault: BreakMode):
-    """FULL arm (blockdiff.py:178-182 through [hf]:656-701) on cat([x_t, x_0]). cos/sin: rotary
-    tables [L, rotary_dim] for positions 0..L-1, shared by both halves."""
-    B, L, _ = n0.shape
-    x = torch.cat([nt, n0], 1)  # [B, 2L, D]
+def _attention_arm(att, n: torch.Tensor, cos, sin, block: int, fault: BreakMode) -> torch.Tensor:
+    """FULL arm (blockdiff.py:178-182 through [hf]:656-701) on cat([x_t, x_0]). n: [2B, L, D] as in
+    the GDN arm; cos/sin: rotary tables [L, rotary_dim] for positions 0..L-1, shared by both halves."""
+    B2, L, D = n.shape
+    B = B2 // 2
+    # [B, 2L, D] = cat([x_t, x_0], 1) per sequence: a view at B = 1
+    x = n.view(2, B, L, D).transpose(0, 1).reshape(B, 2 * L, D)
     S = 2 * L
     hd = att.head_dim
     q, gate = torch.chunk(att.q_proj(x).view(B, S, -1, 2 * hd), 2, dim=-1)
@@ -125,32 +127,44 @@ def _attention_arm(att, n0: torch.Tensor, nt: torch.Tensor, cos, sin, block: int
     v = att.v_proj(x).view(B, S, -1, hd)
     o = attention.bd_attention(q, k, v, block=block, scale=float(att.scaling), leak_xt_prefix=fault.leak_xt_prefix)
     out = att.o_proj(o.reshape(B, S, -1) * torch.sigmoid(gate))
-    return out[:, L:], out[:, :L]
+    return out.view(B, 2, L, -1).transpose(0, 1).reshape(2 * B, L, -1)
+
+
+def layer_step_stacked(layer, kind: str, h: torch.Tensor, *, block: int, cos, sin, fault: BreakMode | None = None,
+                       m: torch.Tensor | None = None):
+    """One decoder layer for both streams held as one tensor h [2B, L, D] (rows 0..B-1 the noised
+    stream, B..2B-1 the clean one), so that every norm, projection and MLP GEMM runs once over both
+    streams. m: the previous layer's MLP output not yet added to h (None: nothing pending); its
+    residual add is fused into this layer's input norm. Returns (h, m) with this layer's MLP
+    output pending."""
+    fault = fault or BreakMode()
+    if m is None:
+        n = rmsnorm(h, layer.input_layernorm)
+    else:
+        n, h = rmsnorm(m, layer.input_layernorm, residual=h)
+    if kind == LINEAR:
+        o = _gdn_fork_arm(layer.linear_attn, n, block, fault)
+    elif kind == FULL:
+        o = _attention_arm(layer.self_attn, n, cos, sin, block, fault)
+    else:
+        raise ValueError(f"unknown layer type {kind}")
+    n, h = rmsnorm(o, layer.post_attention_layernorm, residual=h)
+    return h, mlp(layer.mlp, n)
 
 
 def layer_step(layer, kind: str, h0: torch.Tensor, ht: torch.Tensor, *, block: int, cos, sin,
                fault: BreakMode | None = None, m0: torch.Tensor | None = None, mt: torch.Tensor | None = None):
-    """One decoder layer for both streams (blockdiff.py:147-188). cos/sin: rotary tables
-    [L, rotary_dim] (positions shared by the halves of cat([x_t, x_0])).
+    """One decoder layer for both streams (blockdiff.py:147-188) on separate stream tensors: stacks
+    them and runs `layer_step_stacked`. cos/sin: rotary tables [L, rotary_dim] (positions shared by
+    the halves of cat([x_t, x_0])).
 
     m0/mt: the previous layer's MLP outputs not yet added to h0/ht (None: nothing pending); their
     residual add is fused into this layer's input norm. Returns (h0, ht, m0, mt): the streams
     after the mixer residual and this layer's MLP outputs, again pending."""
-    fault = fault or BreakMode()
-    if m0 is None:
-        n0, nt = rmsnorm(h0, layer.input_layernorm), rmsnorm(ht, layer.input_layernorm)
-    else:
-        n0, h0 = rmsnorm(m0, layer.input_layernorm, residual=h0)
-        nt, ht = rmsnorm(mt, layer.input_layernorm, residual=ht)
-    if kind == LINEAR:
-        o0, ot = _gdn_fork_arm(layer.linear_attn, n0, nt, block, fault)
-    elif kind == FULL:
-        o0, ot = _attention_arm(layer.self_attn, n0, nt, cos, sin, block, fault)
-    else:
-        raise ValueError(f"unknown layer type {kind}")
-    n0, h0 = rmsnorm(o0, layer.post_attention_layernorm, residual=h0)
-    nt, ht = rmsnorm(ot, layer.post_attention_layernorm, residual=ht)
-    return h0, ht, mlp(layer.mlp, n0), mlp(layer.mlp, nt)
+    B = h0.shape[0]
+    m = None if m0 is None else torch.cat([mt, m0], 0)
+    h, m = layer_step_stacked(layer, kind, torch.cat([ht, h0], 0), block=block, cos=cos, sin=sin, fault=fault, m=m)
+    return h[B:], h[:B], m[B:], m[:B]
 
 
 def _forbid_grad(*modules):
@@ -181,21 +195,19 @@ def block_diffusion_forward(text_model, lm_head, x0_ids: torch.Tensor, xt_ids: t
     _forbid_grad(text_model, lm_head)
     del checkpointing
 
-    h0 = text_model.embed_tokens(x0_ids)
-    ht = text_model.embed_tokens(xt_ids)
-    cos, sin = rotary_tables(text_model, L, h0.device, h0.dtype)
+    # both streams as one tensor [2B, L, D]: rows 0..B-1 the noised stream, B..2B-1 the clean one
+    h = text_model.embed_tokens(torch.cat([xt_ids, x0_ids], 0))
+    cos, sin = rotary_tables(text_model, L, h.device, h.dtype)
     n = cfg.num_hidden_layers if layers is None else layers
-    m0 = mt = None
+    m = None
     for i in range(n):
-        h0, ht, m0, mt = layer_step(text_model.layers[i], cfg.layer_types[i], h0, ht, block=block, cos=cos, sin=sin,
-                                    fault=fault, m0=m0, mt=mt)
-    if m0 is None:
-        ht, h0 = rmsnorm(ht, text_model.norm), rmsnorm(h0, text_model.norm)
-    else:
-        ht, h0 = rmsnorm(mt, text_model.norm, residual=ht)[0], rmsnorm(m0, text_model.norm, residual=h0)[0]
+        h, m = layer_step_stacked(text_model.layers[i], cfg.layer_types[i], h, block=block, cos=cos, sin=sin,
+                                  fault=fault, m=m)
+    h = rmsnorm(h, text_model.norm) if m is None else rmsnorm(m, text_model.norm, residual=h)[0]
     if output == "hidden":
-        return ht, h0
-    return lm_head(ht), lm_head(h0)
+        return h[:B], h[B:]
+    logits = lm_head(h)
+    return logits[:B], logits[B:]
 
 
 class LayerStep(nn.Module):

@@ -6,8 +6,8 @@ hipBLASLt solution that measured fastest, with validator lines for the torch, HI
 rocBLAS versions and the GPU architecture it was made with. `enable()` loads it with run-time
 tuning off, so a shape the table lacks keeps the library's default choice. TunableOp rejects the
 table when a validator differs (another library build or GPU). The GEMMs stay library calls; the
-table only chooses among the library's own solutions (the stack's forward measured 61.9 -> 56.6 ms
-on MI355X).
+table only chooses among the library's own solutions (the stack's forward with per-stream MLPs
+measured 61.9 -> 56.6 ms on MI355X).
 """
 
 import os

@@ -259,6 +259,23 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
 }
 
+// The same over rows whose gate and up halves sit ld elements apart row to row (the two halves of
+// one gate | up projection): out [rows, cols] contiguous; cols a multiple of 8.
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const T* __restrict__ g, const T* __restrict__ u,
+                                                          long long ld, T* __restrict__ out, long long rows,
+                                                          long long cols) {
+  typedef __attribute__((ext_vector_type(8))) T V8;
+  const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i >= rows * cols) return;
+  const long long r = i / cols, c = i - r * cols;
+  const V8 gv = *(const V8*)(g + r * ld + c), uv = *(const V8*)(u + r * ld + c);
+  V8 o;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = from_f32<T>(round_through<T>(silu_f32(to_f32(gv[k]))) * to_f32(uv[k]));
+  *(V8*)(out + i) = o;
+}
+
 }  // namespace dllm
 
 using namespace dllm;
@@ -368,6 +385,29 @@ extern "C" int dllm_swiglu_fwd(const void* gate, const void* up, void* out, int6
     swiglu_kernel<bf16><<<dim3((unsigned)nb), dim3(256), 0, st>>>((const bf16*)gate, (const bf16*)up, (bf16*)out, n);
   else if (dtype == DT_F32)
     swiglu_kernel<float><<<dim3((unsigned)nb), dim3(256), 0, st>>>((const float*)gate, (const float*)up, (float*)out, n);
+  else
+    return fail(DLLM_EUNSUPPORTED, "swiglu: dtype %d not supported", dtype);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "swiglu launch: %s", hipGetErrorString(e));
+}
+
+extern "C" int dllm_swiglu_rows_fwd(const void* gate, const void* up, int64_t ld, void* out, int64_t rows,
+                                    int64_t cols, int dtype, void* stream) {
+  if (!gate || !up || !out) return fail(DLLM_EINVAL, "swiglu: null pointer");
+  if (rows < 0 || cols < 0 || ld < cols) return fail(DLLM_EINVAL, "swiglu: bad sizes rows=%lld cols=%lld ld=%lld",
+                                                      (long long)rows, (long long)cols, (long long)ld);
+  if (rows == 0 || cols == 0) return DLLM_OK;
+  if (cols % 8 || ld % 8 || ((uintptr_t)gate | (uintptr_t)up | (uintptr_t)out) % 16)
+    return fail(DLLM_EINVAL, "swiglu: rows must be whole 16-byte vectors (cols, ld multiples of 8, aligned pointers)");
+  const long long nb = (rows * cols + 8 * 256 - 1) / (8 * 256);
+  if (nb > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "swiglu: too large");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DT_BF16)
+    swiglu_rows_kernel<bf16><<<dim3((unsigned)nb), dim3(256), 0, st>>>((const bf16*)gate, (const bf16*)up, ld,
+                                                                       (bf16*)out, rows, cols);
+  else if (dtype == DT_F32)
+    swiglu_rows_kernel<float><<<dim3((unsigned)nb), dim3(256), 0, st>>>((const float*)gate, (const float*)up, ld,
+                                                                        (float*)out, rows, cols);
   else
     return fail(DLLM_EUNSUPPORTED, "swiglu: dtype %d not supported", dtype);
   hipError_t e = hipGetLastError();

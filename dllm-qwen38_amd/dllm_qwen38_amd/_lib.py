@@ -49,6 +49,7 @@ _SIGNATURES = {
     "dllm_gated_rmsnorm_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_float, _c_int,
                                         _c_int, _c_void_p]),
     "dllm_swiglu_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p]),
+    "dllm_swiglu_rows_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
     "dllm_qk_norm_rope_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p]),

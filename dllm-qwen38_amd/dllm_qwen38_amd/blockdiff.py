@@ -76,7 +76,16 @@ def rmsnorm(x: torch.Tensor, norm, residual: torch.Tensor | None = None):
 
 
 def mlp(m, x: torch.Tensor) -> torch.Tensor:
-    """SwiGLU ([hf]:704-717): the two projections, one fused silu-product kernel, the down projection."""
+    """SwiGLU ([hf]:704-717): the two projections, one fused silu-product kernel, the down projection.
+    When the gate and up weights are the halves of one tensor (`model.fuse_gate_up`), the two
+    projections are one GEMM and the silu product reads its halves in place."""
+    w = getattr(m, "gate_up_weight", None)
+    gw, uw = m.gate_proj.weight, m.up_proj.weight
+    if (w is not None and gw.data_ptr() == w.data_ptr()
+            and uw.data_ptr() == w.data_ptr() + gw.numel() * w.element_size() and w.dtype == x.dtype):
+        y = torch.nn.functional.linear(x, w)
+        n = gw.shape[0]
+        return m.down_proj(norms.swiglu(y[..., :n], y[..., n:]))
     return m.down_proj(norms.swiglu(m.gate_proj(x), m.up_proj(x)))
 
 

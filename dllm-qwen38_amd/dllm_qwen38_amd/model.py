@@ -185,7 +185,23 @@ def build(c: HybridConfig, *, device="cuda", dtype=torch.bfloat16, seed: int = 0
     lm_head.to(dtype)
     # decay parameters stay fp32, as in a checkpoint loaded with dtype bf16 they are cast but the
     # mixer upcasts them before use
+    fuse_gate_up(model)
     return model.eval(), lm_head.eval()
+
+
+def fuse_gate_up(model: nn.Module) -> None:
+    """Store each MLP's gate and up weights as the two halves of one [2I, D] tensor (the modules'
+    weights become views of it, so loading a state dict still writes into it), kept as
+    `gate_up_weight`: the stack driver then runs one GEMM for both."""
+    with torch.no_grad():
+        for mod in model.modules():
+            if hasattr(mod, "gate_proj") and hasattr(mod, "up_proj") and mod.gate_proj.bias is None \
+                    and mod.up_proj.bias is None:
+                w = torch.cat([mod.gate_proj.weight, mod.up_proj.weight], 0)
+                n = mod.gate_proj.weight.shape[0]
+                mod.gate_proj.weight = nn.Parameter(w[:n], requires_grad=mod.gate_proj.weight.requires_grad)
+                mod.up_proj.weight = nn.Parameter(w[n:], requires_grad=mod.up_proj.weight.requires_grad)
+                mod.gate_up_weight = w
 
 
 def param_count(model: nn.Module) -> int:

@@ -62,7 +62,21 @@ def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: f
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """round(round(silu(gate)) * up) ([hf]:704-717). gate and up may be the two column halves of one
+    fused gate | up output (rows ld apart, last dim contiguous): read in place."""
     dev = _lib.require_device(gate, up)
+    if (gate.shape == up.shape and gate.dtype == up.dtype and gate.dim() >= 2 and gate.stride(-1) == 1
+            and up.stride(-1) == 1 and gate.stride(-2) == up.stride(-2) and gate.shape[-1] % 8 == 0
+            and gate.stride(-2) % 8 == 0 and not gate.is_contiguous()):
+        cols, ld = gate.shape[-1], gate.stride(-2)
+        rows = gate.numel() // cols
+        lead_ok = all(gate.stride(i) == gate.stride(i + 1) * gate.shape[i + 1] for i in range(gate.dim() - 2))
+        if lead_ok and gate.data_ptr() % 16 == 0 and up.data_ptr() % 16 == 0:
+            out = torch.empty(gate.shape, dtype=gate.dtype, device=dev)
+            _lib.check(_lib.lib().dllm_swiglu_rows_fwd(gate.data_ptr(), up.data_ptr(), ld, out.data_ptr(), rows, cols,
+                                                       _lib.dtype_code(gate.dtype), _lib.stream_handle(dev)),
+                       "dllm_swiglu_rows_fwd")
+            return out
     g, u = _c(gate), _c(up)
     if g.shape != u.shape or g.dtype != u.dtype:
         raise ValueError("gate and up must match")

@@ -207,6 +207,14 @@ int dllm_gdn_gates_fwd(const void* b, const void* a, const void* a_log, const vo
 int dllm_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
 
 /*
+ * The same over rows [rows, cols] whose gate and up rows are ld elements apart (the two halves of
+ * one fused gate | up projection, [hf]:704-717 with both weights in one GEMM): out contiguous;
+ * cols and ld multiples of 8, 16-byte aligned pointers.
+ */
+int dllm_swiglu_rows_fwd(const void* gate, const void* up, int64_t ld, void* out, int64_t rows, int64_t cols,
+                         int dtype, void* stream);
+
+/*
  * Attention prologue: per (token, head) row of q [B,S,Hq,hd] and k [B,S,Hkv,hd] (strides {b,t,h}
  * in elements, last dim contiguous): RMSNorm over hd with (1 + w), then partial RoPE on the first
  * rotary_dim dims, out = a*cos + rotate_half(a)*sin with products and sum rounded to the dtype.

@@ -108,3 +108,16 @@ def test_gdn_gates_match_torch(dev, dtype, pdtype):
     rg = -a_log.float().exp() * torch.nn.functional.softplus(a.float() + dt_bias.float())
     assert ((gg.cpu() - rg).abs() <= 1e-6 * rg.abs() + 1e-30).all()
     assert (a.float() + dt_bias.float() > 20).any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_swiglu_on_the_halves_of_a_fused_projection(dev, dtype):
+    """The row-strided form (gate and up the column halves of one gate | up output) equals the
+    contiguous form bit for bit."""
+    g = torch.Generator().manual_seed(34816)
+    y = torch.randn(3, 40, 2 * 272, generator=g).to(dtype).to(dev)
+    gate, up = y[..., :272], y[..., 272:]
+    assert not gate.is_contiguous()
+    got = norms.swiglu(gate, up)
+    ref = norms.swiglu(gate.contiguous(), up.contiguous())
+    assert got.is_contiguous() and torch.equal(got, ref)

@@ -52,3 +52,20 @@ def test_argument_validation_fails_before_any_launch():
     assert st == -1 and "null pointer" in _lib.last_error()
     st = lib.dllm_fork_layout(1, 33, 32, 4, 1, 1, 1, None)
     assert st == -1 and "not a multiple of block" in _lib.last_error()
+
+
+def test_swiglu_rows_and_decode_linear_validate_before_any_launch():
+    lib = _lib.lib()
+    st = lib.dllm_swiglu_rows_fwd(None, None, 16, None, 1, 8, _lib.DT_BF16, None)
+    assert st == -1 and "null pointer" in _lib.last_error()
+    st = lib.dllm_swiglu_rows_fwd(16, 32, 4, 64, 1, 8, _lib.DT_BF16, None)  # ld < cols
+    assert st == -1 and "bad sizes" in _lib.last_error()
+    st = lib.dllm_swiglu_rows_fwd(16, 32, 12, 64, 1, 12, _lib.DT_BF16, None)  # cols not a multiple of 8
+    assert st == -1 and "16-byte vectors" in _lib.last_error()
+    w = (ctypes.c_void_p * 1)(16)
+    o = (ctypes.c_void_p * 1)(16)
+    n = (ctypes.c_int * 1)(128)
+    st = lib.dllm_decode_linear_multi_fwd(16, 32, 128, 1, w, o, n, None, 4, 0, _lib.DT_BF16, None)
+    assert st == -1 and "workspace" in _lib.last_error()
+    st = lib.dllm_decode_linear_multi_fwd(16, 65, 128, 1, w, o, n, 16, 4, 0, _lib.DT_BF16, None)
+    assert st == -2 and "64 rows" in _lib.last_error()

@@ -158,6 +158,34 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict_
   }
 }
 
+// The same with 16-byte rows: LPR = dim / 8 lanes per row (dim 64 .. 512), 64 / LPR rows per wave,
+// each lane 8 elements of x, z and w; the row's sum of squares by a butterfly over its lanes.
+template <int LPR>
+__global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(const bf16* __restrict__ x, const bf16* __restrict__ z,
+                                                                const bf16* __restrict__ w, bf16* __restrict__ y,
+                                                                int rows, float eps) {
+  constexpr int DIM = 8 * LPR, RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const long long row = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int c0 = (lane % LPR) * 8;
+  const long long base = (row < rows ? row : rows - 1) * DIM + c0;  // every lane takes part in the butterfly
+  const bf16x8 xv = *(const bf16x8*)(x + base), zv = *(const bf16x8*)(z + base), wv = *(const bf16x8*)(w + c0);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf((float)xv[i], (float)xv[i], ss);
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float inv = rsqrtf(ss / (float)DIM + eps);
+  bf16x8 yv;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = round_through<bf16>((float)xv[i] * inv);
+    const float u = round_through<bf16>((float)wv[i] * t);
+    yv[i] = (bf16)(u * silu_f32((float)zv[i]));
+  }
+  if (row < rows) *(bf16x8*)(y + base) = yv;
+}
+
 // Gated DeltaNet gates of every (token, value head): beta = round_T(sigmoid(b)) held in fp32, and
 // g = -exp(A_log) * softplus(a + dt_bias) in fp32 (softplus linear above 20, as torch's).
 template <typename T, typename TP>
@@ -337,8 +365,21 @@ extern "C" int dllm_gated_rmsnorm_fwd(const void* x, const void* z, const void* 
   if (!x || !z || !weight || !y) return fail(DLLM_EINVAL, "gated rmsnorm: null pointer");
   if (rows < 0 || dim <= 0) return fail(DLLM_EINVAL, "gated rmsnorm: bad sizes rows=%d dim=%d", rows, dim);
   if (rows == 0) return DLLM_OK;
-  const dim3 grid((rows + 3) / 4), block(256);
   hipStream_t st = (hipStream_t)stream;
+  const bool vec = ((uintptr_t)x | (uintptr_t)z | (uintptr_t)weight | (uintptr_t)y) % 16 == 0;
+  if (dtype == DT_BF16 && dtype_w == DT_BF16 && vec && (dim == 64 || dim == 128 || dim == 256 || dim == 512)) {
+    const int rpb = 4 * (512 / dim);  // rows per workgroup: 4 waves of 64 / (dim / 8) rows
+    const dim3 g((unsigned)((rows + rpb - 1) / rpb)), b(256);
+    switch (dim) {
+      case 64: gated_rmsnorm_vec_kernel<8><<<g, b, 0, st>>>((const bf16*)x, (const bf16*)z, (const bf16*)weight, (bf16*)y, rows, eps); break;
+      case 128: gated_rmsnorm_vec_kernel<16><<<g, b, 0, st>>>((const bf16*)x, (const bf16*)z, (const bf16*)weight, (bf16*)y, rows, eps); break;
+      case 256: gated_rmsnorm_vec_kernel<32><<<g, b, 0, st>>>((const bf16*)x, (const bf16*)z, (const bf16*)weight, (bf16*)y, rows, eps); break;
+      default: gated_rmsnorm_vec_kernel<64><<<g, b, 0, st>>>((const bf16*)x, (const bf16*)z, (const bf16*)weight, (bf16*)y, rows, eps); break;
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? DLLM_OK : fail(DLLM_ELAUNCH, "gated rmsnorm launch: %s", hipGetErrorString(e));
+  }
+  const dim3 grid((rows + 3) / 4), block(256);
   if (dtype == DT_BF16 && dtype_w == DT_BF16)
     gated_rmsnorm_kernel<bf16, bf16><<<grid, block, 0, st>>>((const bf16*)x, (const bf16*)z, (const bf16*)weight,
                                                             (bf16*)y, rows, dim, eps);

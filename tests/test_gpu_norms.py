@@ -42,11 +42,12 @@ def test_rmsnorm_with_and_without_residual(dev, dtype, rows, dim):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_gated_rmsnorm(dev, dtype):
-    g = torch.Generator().manual_seed(3)
-    x = torch.randn(301, 128, generator=g).to(dtype)
-    z = torch.randn(301, 128, generator=g).to(dtype)
-    w = (1 + 0.1 * torch.randn(128, generator=g)).to(dtype)
+@pytest.mark.parametrize("dim", [128, 64, 512, 96])
+def test_gated_rmsnorm(dev, dtype, dim):
+    g = torch.Generator().manual_seed(3 + dim)
+    x = torch.randn(301, dim, generator=g).to(dtype)
+    z = torch.randn(301, dim, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(dtype)
     y = norms.gated_rmsnorm(x.to(dev), z.to(dev), w.to(dev), 1e-6)
     _close(y, model_ref.gated_rmsnorm(x, z, w, 1e-6), dtype, f"gated rmsnorm {dtype}")
 

@@ -287,6 +287,60 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
 }
 
+// The same for bf16 heads of 256 with 8-byte rows: lane l holds columns 4l .. 4l + 3, so the
+// rotate_half partner of a rotated column (rd / 2 away) sits in lane l ^ (rd / 8) at the same
+// position (rd / 8 a power of two): one lane exchange per element instead of a search over the wave.
+__global__ __launch_bounds__(256) void qk_norm_rope256_kernel(
+    const bf16* __restrict__ q, long long q_sb, int q_st, int q_sh, const bf16* __restrict__ k, long long k_sb,
+    int k_st, int k_sh, const bf16* __restrict__ wq, const bf16* __restrict__ wk, const bf16* __restrict__ cosb,
+    const bf16* __restrict__ sinb, bf16* __restrict__ qo, bf16* __restrict__ ko, int B, int S, int L, int Hq, int Hkv,
+    int rd, float eps) {
+  typedef __attribute__((ext_vector_type(4))) bf16 T4;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const long long nq = (long long)B * S * Hq, nk = (long long)B * S * Hkv;
+  if (row >= nq + nk) return;
+  const bool isq = row < nq;
+  const long long rr = isq ? row : row - nq;
+  const int H = isq ? Hq : Hkv;
+  const int hh = (int)(rr % H);
+  const long long bt = rr / H;
+  const int t = (int)(bt % S), b = (int)(bt / S);
+  const bf16* src = isq ? q + b * q_sb + (long long)t * q_st + (long long)hh * q_sh
+                        : k + b * k_sb + (long long)t * k_st + (long long)hh * k_sh;
+  const bf16* w = isq ? wq : wk;
+  const int c0 = 4 * lane;
+  const T4 xv = *(const T4*)(src + c0);
+  const T4 wv = *(const T4*)(w + c0);
+  float v[4], ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = (float)xv[i];
+    ss = __builtin_fmaf(v[i], v[i], ss);
+  }
+  const float inv = rsqrtf(wave_sum(ss) / 256.f + eps);
+  const int half = rd / 2, pos = t % L;
+  T4 o;
+  float nv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) nv[i] = round_through<bf16>(v[i] * inv * (1.f + (float)wv[i]));
+  float pv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pv[i] = __shfl_xor(nv[i], rd / 8);
+  if (c0 < rd) {
+    const T4 cs = *(const T4*)(cosb + (long long)pos * rd + c0), sn = *(const T4*)(sinb + (long long)pos * rd + c0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float rot = c0 < half ? -pv[i] : pv[i];
+      o[i] = (bf16)round_through<bf16>(round_through<bf16>(nv[i] * (float)cs[i]) + round_through<bf16>(rot * (float)sn[i]));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (bf16)nv[i];
+  }
+  *(T4*)((isq ? qo : ko) + rr * 256 + c0) = o;
+}
+
 // The same over rows whose gate and up halves sit ld elements apart row to row (the two halves of
 // one gate | up projection): out [rows, cols] contiguous; cols a multiple of 8.
 template <typename T>
@@ -474,7 +528,18 @@ extern "C" int dllm_qk_norm_rope_fwd(const void* q, const int64_t* q_strides, co
   const long long nb = (rows + 3) / 4;
   if (nb > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "qk norm rope: too large");
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == DT_BF16 && dtype_w == DT_BF16)
+  const int rd8 = rotary_dim / 8;
+  const bool rd_ok = rotary_dim > 0 && rotary_dim % 8 == 0 && (rd8 & (rd8 - 1)) == 0;
+  const bool al8 = ((uintptr_t)q | (uintptr_t)k | (uintptr_t)q_norm_w | (uintptr_t)k_norm_w | (uintptr_t)cos_table |
+                    (uintptr_t)sin_table | (uintptr_t)q_out | (uintptr_t)k_out) % 8 == 0;
+  bool st4 = true;
+  for (int i = 0; i < 3; ++i) st4 = st4 && q_strides[i] % 4 == 0 && k_strides[i] % 4 == 0;
+  if (dtype == DT_BF16 && dtype_w == DT_BF16 && head_dim == 256 && rd_ok && al8 && st4) {
+    qk_norm_rope256_kernel<<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+        (const bf16*)q, q_strides[0], (int)q_strides[1], (int)q_strides[2], (const bf16*)k, k_strides[0],
+        (int)k_strides[1], (int)k_strides[2], (const bf16*)q_norm_w, (const bf16*)k_norm_w, (const bf16*)cos_table,
+        (const bf16*)sin_table, (bf16*)q_out, (bf16*)k_out, B, S, L, Hq, Hkv, rotary_dim, eps);
+  } else if (dtype == DT_BF16 && dtype_w == DT_BF16)
     qk_norm_rope_kernel<bf16, bf16><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
         (const bf16*)q, q_strides[0], (int)q_strides[1], (int)q_strides[2], (const bf16*)k, k_strides[0],
         (int)k_strides[1], (int)k_strides[2], (const bf16*)q_norm_w, (const bf16*)k_norm_w, (const bf16*)cos_table,

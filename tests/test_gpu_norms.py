@@ -67,7 +67,7 @@ class _Norm:
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("Hq,Hkv,hd,rd", [(4, 2, 16, 4), (6, 2, 256, 64), (3, 1, 128, 32)])
+@pytest.mark.parametrize("Hq,Hkv,hd,rd", [(4, 2, 16, 4), (6, 2, 256, 64), (3, 1, 128, 32), (2, 1, 256, 256), (2, 2, 256, 8)])
 def test_qk_norm_rope(dev, dtype, Hq, Hkv, hd, rd):
     B, L = 2, 24
     S = 2 * L

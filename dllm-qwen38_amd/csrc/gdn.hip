@@ -1412,6 +1412,11 @@ extern "C" int dllm_gdn_fused_fork_supported(int Dk, int block, int dtype) {
   return dtype == DT_F32 || dtype == DT_BF16;
 }
 
+extern "C" int dllm_gdn_state_fork_path(int Dk, int Dv, int block, int dtype) {
+  if (!dllm_gdn_fused_fork_supported(Dk, block, dtype)) return 0;
+  return (dtype == DT_BF16 && Dk == 128 && Dv == 128) ? 2 : 1;
+}
+
 extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                                   const void* v, const int64_t* v_strides, const float* g, const int64_t* g_strides,
                                   const float* beta, const int64_t* beta_strides, const float* initial_state,

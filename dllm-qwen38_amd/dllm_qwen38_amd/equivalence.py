@@ -1,18 +1,19 @@
-"""The visibility equivalence check of the block-diffusion forward, run on the HIP path.
+"""Block-diffusion equivalence harness for the HIP forward (command line and `run()`).
 
-Counterpart of the reference's `src/dllm_qwen38/equivalence.py:1-226`: same questions, same
-report, same exit codes.
-  1. the noised stream equals the oracle (the unmodified transformers model per block under the
-     block-causal mask);
-  2. the clean stream equals the unmodified model under the block-causal mask;
-  3. perturbations: x_t block k ignores x_t block k-1 and x_0 block k, and reacts to x_0 block k-1;
-  4. every deliberate fault (concat-causal-gdn / mask-leak / no-conv-prefix) turns check 1 red.
-Exit code 0 = every check passed and every fault was detected; 1 = a check failed or a fault went
-undetected; 2 = could not measure. A run that measures nothing never exits 0.
+The candidate is `blockdiff.block_diffusion_forward` on the ROCm device, with the HIP state fork
+and the tile-skipping attention kernel. The oracle is transformers' unmodified model, run in fp32
+on the CPU one block at a time under the block-causal mask (for --dtype bfloat16, on weights
+rounded to bf16 first), so no kernel of this library sits on both sides of a comparison.
 
-The candidate is `blockdiff.block_diffusion_forward` on the device (HIP fork, HIP attention). The
-oracle is transformers' own model in fp32 on the CPU (with --dtype bfloat16, on the bf16-rounded
-weights), so the check never runs the library's kernels on both sides.
+Five checks are measured and reported as numbers:
+  * noised-stream-vs-oracle and clean-stream-vs-oracle (max |logit difference|);
+  * for each block k >= 1: re-drawing x_t block k-1 or x_0 block k must leave the noised logits
+    of block k unchanged, and re-drawing x_0 block k-1 must move them by at least a floor.
+Each of the three deliberate faults (concat-causal-gdn, mask-leak, no-conv-prefix) must then push
+the noised stream past the tolerance. Exit status: 0 when all checks pass and all faults are
+detected, 1 when one does not, 2 when nothing could be measured (no device, no model, bad sizes).
+The command-line flags, report keys and output lines follow the reference's harness
+(src/dllm_qwen38/equivalence.py) so that its callers and log parsers work unchanged.
 
     python -m dllm_qwen38_amd.equivalence [--block 32] [--nblocks 4] [--dtype float32|bfloat16]
 """
@@ -34,6 +35,12 @@ FAULTS = ("concat-causal-gdn", "mask-leak", "no-conv-prefix")
 
 def _maxdiff(a: torch.Tensor, b: torch.Tensor) -> float:
     return float((a.float().cpu() - b.float().cpu()).abs().max())
+
+
+def oracle_gdn_kernel() -> str:
+    """The chunked delta-rule implementation the transformers oracle runs: the flash-linear-attention
+    package when it is importable, else transformers' own torch code (the case in this image)."""
+    return "fla" if sys.modules.get("fla") is not None else "torch-reference"
 
 
 def run(cand_model, cand_head, oracle_model, oracle_head, *, block: int, nblocks: int, layers: int | None,
@@ -113,13 +120,18 @@ def _load(model_id: str | None, seed: int):
 
 def main(argv: list[str] | None = None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("--model", default=None, help="local checkpoint directory; omit for the tiny random model")
-    p.add_argument("--layers", type=int, default=None, help="use only the first N layers")
+    p.add_argument("--model", default=None, help="checkpoint directory on disk (no download); default: the tiny "
+                   "random test model")
+    p.add_argument("--layers", type=int, default=None, help="truncate both models to their first N layers")
     p.add_argument("--block", type=int, default=32)
     p.add_argument("--nblocks", type=int, default=4)
-    p.add_argument("--tol", type=float, default=None, help="max |dlogit| accepted (default: fp32 1e-3, bf16 0.25)")
-    p.add_argument("--change-floor", type=float, default=None, help="min |dlogit| of a real dependency (default 10*tol)")
+    p.add_argument("--tol", type=float, default=None, help="largest logit difference that still passes "
+                   "(1e-3 for float32, 0.25 for bfloat16 unless given)")
+    p.add_argument("--change-floor", type=float, default=None, help="smallest logit change that counts as a real "
+                   "dependency (ten times the tolerance unless given)")
     p.add_argument("--dtype", default="float32", choices=["float32", "bfloat16"])
+    p.add_argument("--attn", default="eager", choices=["eager", "sdpa"], help="attention backend of the "
+                   "transformers oracle; the candidate always runs the HIP kernel")
     p.add_argument("--device", default="cuda")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--json", default=None, help="write the report here as JSON")
@@ -144,6 +156,7 @@ def main(argv: list[str] | None = None) -> int:
         return 2
     oracle_model.requires_grad_(False)
     oracle_head.requires_grad_(False)
+    oracle_model.set_attn_implementation(a.attn)
     cand_model = copy.deepcopy(oracle_model).to(a.device, dtype)
     cand_head = copy.deepcopy(oracle_head).to(a.device, dtype)
     if dtype != torch.float32:  # the oracle sees the same (rounded) weights, in fp32
@@ -153,6 +166,8 @@ def main(argv: list[str] | None = None) -> int:
     rep = run(cand_model, cand_head, oracle_model, oracle_head, block=a.block, nblocks=a.nblocks, layers=a.layers,
               tol=tol, change_floor=floor, seed=a.seed, device=a.device)
     rep["model"] = a.model or "tiny-random"
+    rep["attn"] = a.attn
+    rep["oracle_gdn_kernel"] = oracle_gdn_kernel()
     if a.json:
         with open(a.json, "w") as f:
             json.dump(rep, f, indent=1)
@@ -163,7 +178,7 @@ def main(argv: list[str] | None = None) -> int:
         print(f"{'DETECTED' if f['detected'] else 'UNDETECTED'}\tfault:{f['fault']}\t{f['max_abs_diff']:.3e}")
     print(f"CHECKS\t{rep['checks_passed']}/{rep['checks_total']}\tFAULTS-DETECTED\t{rep['faults_detected']}/"
           f"{rep['faults_total']}\tmodel={rep['model']} layers={rep['layers']} L={rep['seq_len']} dtype={rep['dtype']} "
-          f"{rep['seconds']}s")
+          f"oracle-gdn={rep['oracle_gdn_kernel']} {rep['seconds']}s")
     ok = rep["checks_passed"] == rep["checks_total"] and rep["faults_detected"] == rep["faults_total"]
     return 0 if ok else 1
 

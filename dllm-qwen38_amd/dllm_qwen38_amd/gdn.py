@@ -106,12 +106,26 @@ def _core(q, k, v, g, beta, *, chunk_size, initial_state, need_states):
 
 
 def causal_conv1d_fn(hidden_states: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
-                     activation: str | None = None, *, conv_prefix: torch.Tensor | None = None, **kwargs):
+                     activation: str | None = None, seq_idx=None, initial_states: torch.Tensor | None = None,
+                     return_final_states: bool = False, final_states_out: torch.Tensor | None = None, *,
+                     conv_prefix: torch.Tensor | None = None):
     """Causal depthwise conv [B, C, T] -> [B, C, T] (transformers modeling_qwen3_5.py:219-239), with
     an optional [B, C, P] prefix: equal to the conv over cat([prefix, x]) cut to the last T outputs
-    (reference gdn.py:217-219). The result is a [B, C, T] view of token-major [B, T, C] storage."""
+    (reference gdn.py:217-219). The result is a [B, C, T] view of token-major [B, T, C] storage.
+
+    The keyword arguments of the causal-conv1d package's function that the seam may pass are
+    honoured or refused, never dropped: `initial_states` [B, C, K-1] is the prefix under that
+    package's name; `return_final_states` also returns the last K-1 inputs of the extended sequence
+    ([B, C, K-1], written into `final_states_out` when given); `seq_idx` (packed sequences) is
+    not supported and raises."""
     if activation not in (None, "silu", "swish"):
         raise ValueError(f"activation {activation} not supported (silu or None)")
+    if seq_idx is not None:
+        raise NotImplementedError("causal_conv1d_fn: seq_idx (packed sequences) is not supported")
+    if initial_states is not None:
+        if conv_prefix is not None:
+            raise ValueError("pass the prefix once: initial_states and conv_prefix are the same argument")
+        conv_prefix = initial_states
     dev = _lib.require_device(hidden_states, weight, bias, conv_prefix)
     B, C, T = hidden_states.shape
     K = weight.shape[-1]
@@ -128,7 +142,16 @@ def causal_conv1d_fn(hidden_states: torch.Tensor, weight: torch.Tensor, bias: to
         0 if pre is None else pre.shape[2], w.data_ptr(), _lib.ptr(b), y.data_ptr(), B, C, T, K,
         _lib.dtype_code(x.dtype), _lib.dtype_code(w.dtype), int(activation is not None), _lib.stream_handle(dev)),
         "dllm_causal_conv1d_fwd")
-    return y.transpose(1, 2)
+    if not return_final_states:
+        return y.transpose(1, 2)
+    xin = x if pre is None else torch.cat([pre.to(x.dtype), x], 2)
+    if xin.shape[2] < K - 1:
+        xin = torch.cat([xin.new_zeros(B, C, K - 1 - xin.shape[2]), xin], 2)
+    fin = xin[:, :, xin.shape[2] - (K - 1):]
+    if final_states_out is not None:
+        final_states_out.copy_(fin)
+        fin = final_states_out
+    return y.transpose(1, 2), fin
 
 
 def _beta_g(m, b: torch.Tensor, a: torch.Tensor):
@@ -238,7 +261,8 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
             y0.data_ptr(), yt.data_ptr(), L * Cd, Cd, b0.data_ptr(), bt_.data_ptr(), gg0.data_ptr(), ggt.data_ptr(),
             o0.data_ptr(), ot.data_ptr(), _lib.ptr(states), B, L, Hk, Hv, Dk, Dv, block, code, Dk ** -0.5, sh),
             "dllm_gdn_state_fork_fwd")
-        _IMPL["last"], _IMPL["reason"] = "hip", ""
+        path = Lb.dllm_gdn_state_fork_path(Dk, Dv, block, code)
+        _IMPL["last"], _IMPL["reason"] = "hip", _FORK_PATHS.get(path, "")
     else:
         # two-pass fork on the same HIP core: clean pass with states, then the B*nb noised rows
         # relaunched from the shifted states (reference blockdiff.py:160-176)
@@ -259,6 +283,10 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
             states.copy_(st0)
         _IMPL["last"], _IMPL["reason"] = "hip", "two-pass fork (fused kernel does not take this shape)"
     return {"o0": o0, "ot": ot, "states": states, "tails": tails, "y0": y0, "yt": yt}
+
+
+# kernel names reported through last_impl() for the fused fork (dllm_gdn_state_fork_path)
+_FORK_PATHS = {2: "pipelined fork kernel", 1: "fused fork kernel"}
 
 
 def fork_layout(B: int, L: int, block: int, width: int = 4, device="cuda"):

@@ -57,6 +57,15 @@ int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const void* k, c
 int dllm_gdn_fused_fork_supported(int Dk, int block, int dtype);
 
 /*
+ * Which kernel dllm_gdn_state_fork_fwd runs for (Dk, Dv, block, dtype) on 16-byte aligned
+ * activations: 2 = the pipelined fork kernel (bf16 heads of 128 x 128), 1 = the first fused fork
+ * kernel (other shapes dllm_gdn_fused_fork_supported accepts), 0 = neither (the caller runs the
+ * two-pass fork). The reference reports the core it ran through last_impl()
+ * (src/dllm_qwen38/gdn.py:44-45); this is the same report one level down.
+ */
+int dllm_gdn_state_fork_path(int Dk, int Dv, int block, int dtype);
+
+/*
  * Fused state fork of one GDN layer, both streams in one launch.
  * Replaces the LINEAR arm of src/dllm_qwen38/blockdiff.py:153-177 (the clean pass
  * gdn_mixer_forward(need_states=True) at :160, the state shift at :165-166 and the relaunch of

@@ -55,8 +55,13 @@ def chunk_gated_delta_rule_with_states(
     initial_state: torch.Tensor | None = None,
     use_qk_l2norm_in_kernel: bool = True,
     need_states: bool = True,
+    _plant: str | None = None,
 ):
     """(out [B,T,Hv,Dv] in the input dtype, states [B,T/C,Hv,Dk,Dv] fp32 or None).
+
+    `_plant` injects a deliberate mistake for tests that check a tolerance can see it:
+    "drop-carry" (the update forgets e^gamma_last S) or "carry-scale" (the carried state is scaled
+    by 1.05). Never used to produce expected values.
 
     Per chunk i and head: with gamma = cumsum(g) inside the chunk and
     Gamma[r,s] = exp(gamma_r - gamma_s) for s <= r (else 0),
@@ -107,7 +112,12 @@ def chunk_gated_delta_rule_with_states(
     for i in range(n):
         v_new = U[:, :, i] - W[:, :, i] @ S
         out[:, :, i] = q_dec[:, :, i] @ S + P[:, :, i] @ v_new
-        S = S * lam[:, :, i] + k_dec[:, :, i].transpose(-1, -2) @ v_new
+        carry = S * lam[:, :, i]
+        if _plant == "drop-carry":
+            carry = torch.zeros_like(carry)
+        elif _plant == "carry-scale":
+            carry = carry * 1.05
+        S = carry + k_dec[:, :, i].transpose(-1, -2) @ v_new
         if need_states:
             snaps.append(S)
     out = out.reshape(B, Hv, T, Dv).transpose(1, 2).to(out_dtype).contiguous()
@@ -243,25 +253,28 @@ def _split_heads(mixed, B, T, Hk, Hv, Dk, Dv):
 
 
 def gdn_conv_core(raw, conv_w, beta, g, *, Hk, Hv, Dk, Dv, chunk, conv_prefix=None,
-                  initial_state=None, need_states=True):
+                  initial_state=None, need_states=True, _plant=None):
     """One mixer pass without projections: raw [B,T,conv_dim] (token-major) -> conv+SiLU (with an
     optional [B,conv_dim,K-1] prefix) -> split/GQA -> chunked core. Returns (o, states)."""
     B, T, _ = raw.shape
     mixed = causal_conv1d(raw.transpose(1, 2), conv_w, None, "silu", prefix=conv_prefix).transpose(1, 2)
     q, k, v = _split_heads(mixed, B, T, Hk, Hv, Dk, Dv)
     return chunk_gated_delta_rule_with_states(q, k, v, g, beta, chunk_size=chunk,
-                                              initial_state=initial_state, need_states=need_states)
+                                              initial_state=initial_state, need_states=need_states,
+                                              _plant=_plant)
 
 
 def state_fork_layer(raw0, rawt, conv_w, beta0, betat, g0, gt, *, Hk, Hv, Dk, Dv, block,
-                     fault: str | None = None, need_states: bool = True):
+                     fault: str | None = None, need_states: bool = True, _plant: str | None = None):
     """The state-fork GDN layer on pre-conv projections of both streams.
 
     raw0/rawt [B,L,conv_dim]; beta*, g* [B,L,Hv]; conv_w [conv_dim,K].
     Returns (o0 [B,L,Hv,Dv], ot [B,L,Hv,Dv], states0 [B,nb,Hv,Dk,Dv] fp32, tails [B*nb,conv_dim,K-1]).
 
     fault: None | "no-conv-prefix" (noised rows' conv starts cold) | "concat-causal-gdn"
-    (one causal pass over cat([x_t, x_0])) — reference blockdiff.py:69-88,155-157,168-170."""
+    (one causal pass over cat([x_t, x_0])) — reference blockdiff.py:69-88,155-157,168-170.
+    `_plant` (tests of tolerances only): the core's "drop-carry" / "carry-scale" on the clean pass,
+    or "fork-off-by-one" (noised block k starts from the clean state after block k, not k-1)."""
     B, L, Cd = raw0.shape
     if L % block:
         raise ValueError(f"L={L} is not a multiple of block={block}")
@@ -272,8 +285,11 @@ def state_fork_layer(raw0, rawt, conv_w, beta0, betat, g0, gt, *, Hk, Hv, Dk, Dv
         o, _ = gdn_conv_core(torch.cat([rawt, raw0], 1), conv_w, torch.cat([betat, beta0], 1),
                              torch.cat([gt, g0], 1), chunk=block, need_states=False, **dims)
         return o[:, L:], o[:, :L], None, None
-    o0, states0 = gdn_conv_core(raw0, conv_w, beta0, g0, chunk=block, need_states=True, **dims)
+    core_plant = _plant if _plant in ("drop-carry", "carry-scale") else None
+    o0, states0 = gdn_conv_core(raw0, conv_w, beta0, g0, chunk=block, need_states=True, _plant=core_plant, **dims)
     init = torch.cat([torch.zeros_like(states0[:, :1]), states0[:, :-1]], 1).reshape(B * nb, Hv, Dk, Dv)
+    if _plant == "fork-off-by-one":
+        init = states0.reshape(B * nb, Hv, Dk, Dv)
     raw0_t = raw0.transpose(1, 2)  # [B, Cd, L], the reference's raw_qkv layout
     padded = torch.cat([torch.zeros_like(raw0_t[:, :, : K - 1]), raw0_t], 2)
     tails = padded.unfold(2, K - 1, block)[:, :, :nb].permute(0, 2, 1, 3).reshape(B * nb, Cd, K - 1)

@@ -69,3 +69,12 @@ def test_swiglu_rows_and_decode_linear_validate_before_any_launch():
     assert st == -1 and "workspace" in _lib.last_error()
     st = lib.dllm_decode_linear_multi_fwd(16, 65, 128, 1, w, o, n, 16, 4, 0, _lib.DT_BF16, None)
     assert st == -2 and "64 rows" in _lib.last_error()
+
+
+def test_fork_path_query():
+    lib = _lib.lib()
+    assert lib.dllm_gdn_state_fork_path(128, 128, 32, _lib.DT_BF16) == 2
+    assert lib.dllm_gdn_state_fork_path(128, 128, 8, _lib.DT_BF16) == 2
+    assert lib.dllm_gdn_state_fork_path(64, 64, 32, _lib.DT_BF16) == 1
+    assert lib.dllm_gdn_state_fork_path(64, 64, 32, _lib.DT_F32) == 1
+    assert lib.dllm_gdn_state_fork_path(128, 128, 64, _lib.DT_BF16) == 0

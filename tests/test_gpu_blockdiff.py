@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from _tiny import noised_ids, tiny_hf_model
-from dllm_qwen38_amd import blockdiff
+from dllm_qwen38_amd import blockdiff, gdn
 from dllm_qwen38_amd import model as hybrid
 from oracle import model_ref
 
@@ -189,3 +189,93 @@ def test_equivalence_harness_passes_and_detects_every_fault(dev, tmp_path):
     out16 = tmp_path / "eq16.json"
     assert equivalence.main(["--dtype", "bfloat16", "--block", "16", "--nblocks", "4", "--change-floor", "1e-3",
                              "--json", str(out16)]) == 0
+
+
+def test_batched_forward_equals_per_row_and_oracle(dev):
+    """The reference's structural check (tests/test_equivalence.py:30-47) on the HIP path: B = 3
+    rows in one forward equal three one-row forwards, and match the per-block oracle."""
+    model, lm_head = tiny_hf_model(seed=2)
+    import copy
+
+    gm, gl = copy.deepcopy(model).to(dev), copy.deepcopy(lm_head).to(dev)
+    block, nb, B = 8, 3, 3
+    g = torch.Generator().manual_seed(2)
+    x0 = torch.randint(0, 256, (B, block * nb), generator=g)
+    xt = x0.clone()
+    xt[torch.rand(B, block * nb, generator=g) < 0.5] = 255
+    with torch.no_grad():
+        lt, l0 = blockdiff.block_diffusion_forward(gm, gl, x0.to(dev), xt.to(dev), block)
+        rows = [blockdiff.block_diffusion_forward(gm, gl, x0[i:i + 1].to(dev), xt[i:i + 1].to(dev), block)[0]
+                for i in range(B)]
+    torch.cuda.synchronize()
+    ref = model_ref.reference_block_logits(model, lm_head, x0, xt, block)
+    assert lt.shape == (B, block * nb, 256)
+    d_rows, d_ref = _maxdiff(lt, torch.cat(rows, 0)), _maxdiff(lt, ref)
+    print(f"batched vs per-row {d_rows:.2e}, vs per-block oracle {d_ref:.2e}")
+    assert d_rows < 1e-5
+    assert d_ref < F32_TOL
+
+
+def test_gdn_mixer_need_states_false_matches_true(tiny_gpu, dev):
+    """gdn_mixer_forward with need_states True/False (reference tests/test_equivalence.py:68-84):
+    bitwise-equal outputs, states [B, n_chunks, Hv, Dk, Dv] or None, raw_qkv of equal shape."""
+    gm, _ = tiny_gpu
+    m = gm.layers[0].linear_attn
+    hs = torch.randn(2, 16, gm.config.hidden_size, generator=torch.Generator().manual_seed(4)).to(dev)
+    with torch.no_grad():
+        o1, s1, raw1 = gdn.gdn_mixer_forward(m, hs, chunk_size=16, need_states=True)
+        o2, s2, raw2 = gdn.gdn_mixer_forward(m, hs, chunk_size=16, need_states=False)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert s1.shape == (2, 1, m.num_v_heads, m.head_k_dim, m.head_v_dim)
+    assert s2 is None
+    assert raw1.shape == raw2.shape == (2, m.conv_dim, 16)
+    assert gdn.last_impl()[0] == "hip"
+
+
+@pytest.mark.parametrize("chunk", [8, 16])
+def test_gdn_mixer_prefix_and_initial_state_vs_oracle(tiny_cpu, tiny_gpu, dev, chunk):
+    """gdn_mixer_forward with a conv prefix and an initial state, as the fork's noised rows call it
+    (reference blockdiff.py:174-176), against the oracle mixer on the CPU."""
+    model, _ = tiny_cpu
+    gm, _ = tiny_gpu
+    m_cpu, m = model.layers[1].linear_attn, gm.layers[1].linear_attn
+    g = torch.Generator().manual_seed(40 + chunk)
+    B, T = 3, 32
+    hs = torch.randn(B, T, gm.config.hidden_size, generator=g)
+    pre = torch.randn(B, m.conv_dim, m.conv_kernel_size - 1, generator=g)
+    init = 0.5 * torch.randn(B, m.num_v_heads, m.head_k_dim, m.head_v_dim, generator=g)
+    with torch.no_grad():
+        o, st, raw = gdn.gdn_mixer_forward(m, hs.to(dev), chunk_size=chunk, conv_prefix=pre.to(dev),
+                                           initial_state=init.to(dev))
+        ro, rst, rraw = model_ref.gdn_mixer(m_cpu, hs, chunk=chunk, conv_prefix=pre, initial_state=init)
+    torch.cuda.synchronize()
+    d = (_maxdiff(o, ro), _maxdiff(st, rst), _maxdiff(raw, rraw))
+    print(f"chunk {chunk}: out {d[0]:.2e} states {d[1]:.2e} raw {d[2]:.2e}")
+    assert max(d) <= F32_TOL
+    # the prefix and the initial state both matter here
+    with torch.no_grad():
+        o_cold, _, _ = gdn.gdn_mixer_forward(m, hs.to(dev), chunk_size=chunk)
+    assert _maxdiff(o, o_cold) > FAULT_MIN
+
+
+def test_equivalence_harness_layer_truncation_and_report(dev, tmp_path):
+    """--layers N runs the first N layers only and says so (reference tests/test_equivalence.py:
+    22-27); the report names the oracle's attention backend and GDN core."""
+    import json
+
+    from dllm_qwen38_amd import equivalence
+
+    out = tmp_path / "eq3.json"
+    rc = equivalence.main(["--layers", "3", "--block", "8", "--nblocks", "2", "--seed", "1", "--change-floor", "0.05",
+                           "--attn", "sdpa", "--json", str(out)])
+    rep = json.loads(out.read_text())
+    assert rep["layers"] == 3
+    assert rep["layer_types"] == ["linear_attention"] * 3
+    assert rep["checks_passed"] == rep["checks_total"] == 5
+    # three GDN layers hold no attention layer, so the mask-leak fault has nothing to break and the
+    # harness reports it undetected (exit 1) rather than claiming a detection it cannot make
+    assert [f["fault"] for f in rep["faults"] if not f["detected"]] == ["mask-leak"]
+    assert rc == 1
+    assert rep["attn"] == "sdpa"
+    assert rep["oracle_gdn_kernel"] == "torch-reference"

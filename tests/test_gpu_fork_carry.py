@@ -1,0 +1,131 @@
+"""GPU parity of the bf16 state-fork kernels where the carried state matters.
+
+The 27B- and 0.8B-class workloads decay 25-45 nats per 32-token block, so the state a block
+inherits is ~1e-11 of its own contribution and a wrong carry would not show. These tests drive
+the same kernels with slow decay, g = -softplus(N(0,1) - 4) (about 0.9 nats per block), over 32
+blocks, and compare with the fp32 oracle on the same bf16 inputs within the bounds of
+tests/_bounds.py (which a dropped, mis-scaled or mis-forked carry exceeds: tests/test_oracle_gdn.py).
+They cover the pipelined fork kernel at both head layouts, at blocks 32, 16 and 8 and without
+state snapshots, and the bf16 chunk kernel (one and two column windows per head) with an
+initial state.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _bounds import excess, out_bound, state_bound
+from dllm_qwen38_amd import gdn, inputs
+from oracle import gdn_ref
+
+pytestmark = pytest.mark.gpu
+
+SLOW = -4.0
+
+
+def _shape(name, B, L, block, Hk, Hv, seed):
+    return inputs.GdnShape(name, B, L, block, Hk, Hv, 128, 4, torch.bfloat16, SLOW, seed)
+
+
+def _fork(s, x, dev, **kw):
+    xd = {k: v.to(dev) for k, v in x.items()}
+    r = gdn.gdn_state_fork(xd["raw0"], xd["rawt"], xd["conv_w"], xd["beta0"], xd["betat"], xd["g0"], xd["gt"],
+                           num_k_heads=s.Hk, num_v_heads=s.Hv, head_k_dim=s.D, head_v_dim=s.D, block=s.block, **kw)
+    torch.cuda.synchronize()
+    return {k: (v.cpu() if v is not None else None) for k, v in r.items()}
+
+
+def _oracle(s, x):
+    return gdn_ref.state_fork_layer(x["raw0"], x["rawt"], x["conv_w"], x["beta0"], x["betat"], x["g0"], x["gt"],
+                                    Hk=s.Hk, Hv=s.Hv, Dk=s.D, Dv=s.D, block=s.block)
+
+
+def _check(name, got, ref, bound):
+    over, ratio = excess(got, ref, bound)
+    d = (got.float() - ref.float()).abs()
+    print(f"{name}: max|d|={d.max().item():.3e} mean|d|={d.mean().item():.3e} max|ref|={ref.float().abs().max().item():.3e} "
+          f"max |d|/bound={ratio:.3f}", flush=True)
+    assert over <= 0, f"{name} exceeds its bf16 bound (max |d|/bound = {ratio:.3f})"
+
+
+CARRY_SHAPES = [
+    _shape("27B-class heads (Hk 16, Hv 48)", 1, 1024, 32, 16, 48, 3150),
+    _shape("0.8B-class heads (Hk = Hv = 16)", 2, 1024, 32, 16, 16, 2150),
+]
+
+
+@pytest.mark.parametrize("s", CARRY_SHAPES, ids=["27b", "08b"])
+def test_pipe_fork_slow_decay_matches_oracle(dev, s):
+    x = inputs.gdn_layer_inputs(s)
+    r = _fork(s, x, dev)
+    assert gdn.last_impl() == ("hip", "pipelined fork kernel")
+    o0, ot, st, tails = _oracle(s, x)
+    assert torch.equal(r["tails"], tails)
+    assert st.abs().max().item() > 0.5, "the carried state must be non-negligible"
+    _check(f"{s.name} o0", r["o0"], o0, out_bound)
+    _check(f"{s.name} ot", r["ot"], ot, out_bound)
+    _check(f"{s.name} states", r["states"], st, state_bound)
+
+
+def test_pipe_fork_clean_stream_vs_float64_recurrence(dev):
+    """The clean outputs and every block state of the pipelined kernel against the float64 token
+    recurrence on the same (bf16-rounded, convolved) inputs: an independent algorithm."""
+    s = CARRY_SHAPES[1]
+    x = inputs.gdn_layer_inputs(s, B=1)
+    r = _fork(s, x, dev)
+    y = gdn_ref.causal_conv1d(x["raw0"].transpose(1, 2), x["conv_w"]).transpose(1, 2)
+    q, k, v = gdn_ref._split_heads(y, 1, s.L, s.Hk, s.Hv, s.D, s.D)
+    ro, rs = gdn_ref.recurrent_gated_delta_rule_f64(q, k, v, x["g0"], x["beta0"], chunk_size=32)
+    _check("clean vs f64 o0", r["o0"], torch.from_numpy(ro), out_bound)
+    _check("clean vs f64 states", r["states"], torch.from_numpy(rs), state_bound)
+
+
+@pytest.mark.parametrize("block", [16, 8])
+def test_pipe_fork_subtile_blocks(dev, block):
+    """Blocks shorter than the 32-row tile (zero-padded rows) through the pipelined kernel."""
+    s = _shape(f"Hk 4, Hv 8, block {block}", 2, 256, block, 4, 8, 4150 + block)
+    x = inputs.gdn_layer_inputs(s)
+    r = _fork(s, x, dev)
+    assert gdn.last_impl() == ("hip", "pipelined fork kernel")
+    o0, ot, st, tails = _oracle(s, x)
+    assert torch.equal(r["tails"], tails)
+    assert r["states"].shape == (2, 256 // block, 8, 128, 128)
+    _check(f"block {block} o0", r["o0"], o0, out_bound)
+    _check(f"block {block} ot", r["ot"], ot, out_bound)
+    _check(f"block {block} states", r["states"], st, state_bound)
+
+
+def test_pipe_fork_need_states_false_is_bit_identical(dev):
+    """The product forward runs the fork without snapshots (states == NULL): same outputs, bitwise."""
+    s = _shape("27B-class heads, L 512", 1, 512, 32, 16, 48, 6150)
+    x = inputs.gdn_layer_inputs(s)
+    a = _fork(s, x, dev)
+    b = _fork(s, x, dev, need_states=False, need_tails=False)
+    assert b["states"] is None and b["tails"] is None
+    assert gdn.last_impl() == ("hip", "pipelined fork kernel")
+    assert torch.equal(a["o0"], b["o0"]) and torch.equal(a["ot"], b["ot"])
+
+
+@pytest.mark.parametrize("B,Hk,Hv", [(1, 2, 8), (2, 16, 64)], ids=["two-windows", "one-window"])
+@pytest.mark.parametrize("chunk", [32, 64])
+def test_chunk_kernel_bf16_matches_oracle(dev, B, Hk, Hv, chunk):
+    """chunk_gated_delta_rule_with_states in bf16 at Dk = Dv = 128 with an initial state and slow
+    decay: fewer than 128 (sequence, head) pairs run two 64-column windows per head, more run one
+    128-column window (the decoder and the two-pass fork use both)."""
+    T = 512
+    q, k, v, g, beta = inputs.gdn_core_inputs(B, T, Hk, Hv, 128, torch.bfloat16, seed=7150 + Hv + chunk,
+                                              g_shift=SLOW)
+    init = torch.randn(B, Hv, 128, 128, generator=torch.Generator().manual_seed(7160 + Hv)) * 0.5
+    out, st = gdn.chunk_gated_delta_rule_with_states(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), chunk,
+                                                     initial_state=init.to(dev))
+    torch.cuda.synchronize()
+    n = Hv // Hk
+    ro, rs = gdn_ref.chunk_gated_delta_rule_with_states(q.repeat_interleave(n, 2), k.repeat_interleave(n, 2), v, g,
+                                                        beta, chunk, initial_state=init)
+    assert st.shape == (B, T // chunk, Hv, 128, 128)
+    # the initial state still weighs on the last chunk's state
+    lam_total = np.exp(g.double().sum(1).max().item())
+    print(f"initial-state weight at the end: {lam_total:.2e}")
+    _check(f"chunk {chunk} {B}x{Hv} out", out.cpu(), ro, out_bound)
+    _check(f"chunk {chunk} {B}x{Hv} states", st.cpu(), rs, state_bound)
+

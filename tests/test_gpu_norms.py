@@ -73,7 +73,7 @@ def test_qk_norm_rope(dev, dtype, Hq, Hkv, hd, rd):
     S = 2 * L
     g = torch.Generator().manual_seed(hd + rd)
     qg = torch.randn(B, S, Hq, 2 * hd, generator=g).to(dtype)  # q_proj output with the gate half
-    q = qg[..., :hd]  # strided view, as the layer passes it
+    q = qg[..., :hd]
     k = torch.randn(B, S, Hkv, hd, generator=g).to(dtype)
     wq = (0.1 * torch.randn(hd, generator=g)).to(dtype)
     wk = (0.1 * torch.randn(hd, generator=g)).to(dtype)
@@ -81,7 +81,11 @@ def test_qk_norm_rope(dev, dtype, Hq, Hkv, hd, rd):
     fr = torch.arange(L, dtype=torch.float32)[:, None] * inv[None, :]
     emb = torch.cat([fr, fr], -1)
     cos, sin = emb.cos().to(dtype), emb.sin().to(dtype)
-    qo, ko = norms.qk_norm_rope(q.to(dev), k.to(dev), _Norm(wq.to(dev)), _Norm(wk.to(dev)), cos.to(dev), sin.to(dev), L)
+    # the strided view is built on the device, as the layer passes it (row stride 2*hd inside a
+    # token of Hq*2*hd): a .to(dev) of the CPU view would make a dense copy
+    qd = qg.to(dev)[..., :hd]
+    assert qd.stride(-2) == 2 * hd and qd.stride(1) == Hq * 2 * hd
+    qo, ko = norms.qk_norm_rope(qd, k.to(dev), _Norm(wq.to(dev)), _Norm(wk.to(dev)), cos.to(dev), sin.to(dev), L)
     c2, s2 = torch.cat([cos, cos]), torch.cat([sin, sin])
     q_ref = attn_ref.apply_rope(model_ref.rmsnorm(q, wq, 1e-6), c2, s2)
     k_ref = attn_ref.apply_rope(model_ref.rmsnorm(k, wk, 1e-6), c2, s2)

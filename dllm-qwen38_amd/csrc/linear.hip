@@ -28,6 +28,8 @@
 //     (gate | up) the second kernel writes round(round(silu(gate)) * up), the MLP's activation,
 //     over the whole gate projection (whole tiles were stored rounded, the up tiles in the
 //     workspace).
+#include <mutex>
+
 #include "common.h"
 
 namespace dllm {
@@ -353,4 +355,72 @@ extern "C" int dllm_decode_linear_fwd(const void* x, const void* weight, void* y
   void* o[1] = {y};
   const int n[1] = {N};
   return dllm_decode_linear_multi_fwd(x, M, K, 1, w, o, n, workspace, workgroups, 0, dtype, stream);
+}
+
+// ---- allocation-free variant: the split-tile pieces live in a fixed per-device array ----------
+//
+// For callers that cannot allocate device memory (code under HIP graph capture, serving loops
+// that forbid it). The pieces a launch needs are G x 2 x 16 KB (two per workgroup), so the array
+// holds 8 MiB = 256 workgroups (one per CU, what dllm_decode_linear_workgroups returns for every
+// projection that splits tiles). Every piece the fixup reads is written by the main kernel of the
+// same call before it on the same stream, so nothing needs clearing; calls that overlap on one
+// GPU (two streams at once) share the array and race.
+namespace dllm {
+constexpr long long LIN_SCRATCH_BYTES = 8LL << 20;
+static __device__ __align__(256) unsigned char scratch[LIN_SCRATCH_BYTES];
+constexpr int LIN_MAX_DEVICES = 64;
+static void* g_scratch_addr[LIN_MAX_DEVICES];  // device address of `scratch` per device, looked up once
+static std::mutex g_scratch_mu;
+
+// Device address of the array on the current device (which must own `stream`).
+static int scratch_address(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear (no-alloc): hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= LIN_MAX_DEVICES) return fail(DLLM_EUNSUPPORTED, "decode linear (no-alloc): device %d", dev);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) return fail(DLLM_EINVAL, "decode linear (no-alloc): hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(DLLM_EINVAL, "decode linear (no-alloc): the stream belongs to device %d, the current device is %d",
+                  (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(DLLM_ELAUNCH, "decode linear (no-alloc): hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return DLLM_OK;
+}
+}  // namespace dllm
+
+extern "C" long long dllm_decode_linear_noalloc_max_bytes(void) { return LIN_SCRATCH_BYTES; }
+
+extern "C" int dllm_decode_linear_fwd_noalloc(const void* x, const void* weight, void* y, int M, int N, int K,
+                                              int workgroups, int dtype, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0 || workgroups <= 0)
+    return fail(DLLM_EINVAL, "decode linear (no-alloc): bad sizes M=%d N=%d K=%d workgroups=%d", M, N, K, workgroups);
+  if (K % 64) return fail(DLLM_EUNSUPPORTED, "decode linear (no-alloc): K=%d is not a multiple of 64", K);
+  // the pieces this launch writes: none when every workgroup's unit range is whole tiles
+  const long long units = lin_units(M, (N + 127) / 128, K);
+  if (units > 0x7fffffffLL) return fail(DLLM_EUNSUPPORTED, "decode linear (no-alloc): %lld work units is too many", units);
+  const long long G = workgroups < units ? workgroups : units;
+  const long long ns = K / 64;
+  bool split = false;
+  for (long long b = 1; b < G && !split; ++b) split = (b * units / G) % ns != 0;
+  const long long need = split ? G * 2 * LIN_TILE * (long long)sizeof(float) : 0;
+  if (need > LIN_SCRATCH_BYTES)
+    return fail(DLLM_EUNSUPPORTED,
+                "decode linear (no-alloc): %lld workgroups splitting tiles need %lld bytes of scratch, more than the "
+                "%lld-byte array (at most %lld such workgroups)", G, need, LIN_SCRATCH_BYTES,
+                LIN_SCRATCH_BYTES / (2 * LIN_TILE * (long long)sizeof(float)));
+  void* ws = nullptr;
+  const int rc = scratch_address(stream, &ws);
+  if (rc != DLLM_OK) return rc;
+  return dllm_decode_linear_fwd(x, weight, y, ws, M, N, K, workgroups, dtype, stream);
 }

@@ -61,6 +61,9 @@ _SIGNATURES = {
     "dllm_decode_linear_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int]),
     "dllm_decode_linear_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_void_p]),
+    "dllm_decode_linear_noalloc_max_bytes": (_c_i64, []),
+    "dllm_decode_linear_fwd_noalloc": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                                _c_void_p]),
     "dllm_decode_linear_multi_fwd": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_voidpp, _c_voidpp, _c_intp,
                                               _c_void_p, _c_int, _c_int, _c_int, _c_void_p]),
     "dllm_gdn_gates_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int,

@@ -171,6 +171,19 @@ int dllm_decode_linear_fwd(const void* x, const void* weight, void* y, void* wor
                            int workgroups, int dtype, void* stream);
 
 /*
+ * dllm_decode_linear_fwd without a workspace argument: no counterpart in the reference. For callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops that forbid
+ * allocation). The split-tile pieces go to a fixed per-device array inside the library of
+ * dllm_decode_linear_noalloc_max_bytes() bytes (8 MiB: 256 workgroups that split tiles, one per
+ * CU); a launch needing more returns -2 with a message, and one that splits no tile has no limit.
+ * Nothing is allocated. The current device must own `stream`. Calls that overlap on one GPU (two
+ * streams at once) share the array and race.
+ */
+long long dllm_decode_linear_noalloc_max_bytes(void);
+int dllm_decode_linear_fwd_noalloc(const void* x, const void* weight, void* y, int M, int N, int K, int workgroups,
+                                   int dtype, void* stream);
+
+/*
  * Up to four projections of the same x in one launch (q | k | v; in_proj_qkv | z | b | a; gate |
  * up): weights[i] [Ns[i], K] -> outs[i] [M, Ns[i]], one workgroup count for all (from
  * dllm_decode_linear_workgroups(M, sum of Ns rounded up to 128, K)); workspace of

@@ -31,16 +31,16 @@ HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 
-def _traffic_from_profiles():
-    """HBM bytes per launch of the fork kernel from the committed PMC summary, if present."""
-    p = os.path.join(ROOT, "profiles", "gdn_fork_27b_traffic.json")
+def _traffic_from_profiles(name):
+    """HBM bytes per launch of the dominant kernel from a committed PMC summary, if present."""
+    p = os.path.join(ROOT, "profiles", name)
     if os.path.exists(p):
         with open(p) as f:
             return json.load(f).get("bytes_per_launch")
     return None
 
 
-def cpu_baseline(sample_L: int, budget_s: float):
+def cpu_baseline(s, sample_L: int, budget_s: float):
     """The CPU oracle (torch fp32 on all host cores of this process) on one sequence of the workload
     (B=1, L=sample_L), re-run until `budget_s` seconds of CPU time have elapsed (at least 3 runs);
     median tokens/s."""
@@ -52,7 +52,6 @@ def cpu_baseline(sample_L: int, budget_s: float):
 
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
-    s = inputs.GDN_27B_BF16
     x = inputs.gdn_layer_inputs(s, B=1, L=sample_L)
     args = (x["raw0"], x["rawt"], x["conv_w"], x["beta0"], x["betat"], x["g0"], x["gt"])
     kw = dict(Hk=s.Hk, Hv=s.Hv, Dk=s.D, Dv=s.D, block=s.block)
@@ -65,9 +64,10 @@ def cpu_baseline(sample_L: int, budget_s: float):
         times.append(time.perf_counter() - t)
     med = statistics.median(times)
     return {"value": sample_L / med, "unit": "tokens/s", "cores": n, "kind": "port",
-            "sample": f"one sequence (B=1 L={sample_L}) of the 27B-class shape (Hk=16 Hv=48 D=128 block 32), "
-                      f"bf16-rounded inputs, fp32 torch CPU oracle on {n} threads; median of {len(times)} runs "
-                      f"after 1 warm-up ({med:.2f} s/run, {sum(times):.1f} s timed)"}
+            "sample": f"one sequence (B=1 L={sample_L}) of the workload's shape (Hk={s.Hk} Hv={s.Hv} D={s.D} "
+                      f"block {s.block}), bf16-rounded inputs, fp32 torch CPU oracle on {n} threads; median of "
+                      f"{len(times)} runs after 1 warm-up ({med:.2f} s/run, {sum(times):.1f} s timed)",
+            **_host_info()}
 
 
 def main(argv=None):
@@ -81,8 +81,10 @@ def main(argv=None):
     ap.add_argument("--calibration-copy-gib", type=float, default=0.0,
                     help="after the timed steps, copy this many GiB device-to-device (the reference transfer "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
-    ap.add_argument("--workload", default="gdn-layer", choices=["gdn-layer", "attention", "stack", "decode"],
-                    help="gdn-layer (default, the headline metric); attention: the complementary-mask attention "
+    ap.add_argument("--workload", default="gdn-layer",
+                    choices=["gdn-layer", "gdn-layer-08b", "attention", "stack", "decode"],
+                    help="gdn-layer (default, the headline metric); gdn-layer-08b: the same layer at the 0.8B-class "
+                         "shape (B=8 L=2048 Hk=Hv=16 D=128); attention: the complementary-mask attention "
                          "layer kernel at B=2 L=4096 Hq=24 Hkv=4 d=256; stack: the 16-layer 27B-class "
                          "two-stream forward at B=1 L=2048; decode: one cached denoising step of that stack "
                          "(a 32-token block over a 2048-token clean prefix)")
@@ -100,22 +102,57 @@ def main(argv=None):
         a.gemm_table = gemm_tuning.enable()
         return bench_stack(a) if a.workload == "stack" else bench_decode(a)
 
+    return bench_gdn_layer(a)
+
+
+def _host_info():
+    """CPU model and torch version of this host, for the cpu_baseline record."""
+    import platform
+
+    import torch
+
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "torch": torch.__version__}
+
+
+GDN_WORKLOADS = {
+    "gdn-layer": ("GDN_27B_BF16", "state-fork GDN layer tokens/s at 27B-class shape; % MFMA/HBM roofline",
+                  "state-fork GDN layer, 27B-class: B=4 L=4096 block=chunk=32 Hk=16 Hv=48 Dk=Dv=128 conv width 4, "
+                  "bf16 in/out, fp32 state", "gdn_fork_27b_traffic.json"),
+    "gdn-layer-08b": ("GDN_08B_BF16", "state-fork GDN layer tokens/s at 0.8B-class shape; % MFMA/HBM roofline",
+                      "state-fork GDN layer, 0.8B-class: B=8 L=2048 block=chunk=32 Hk=Hv=16 Dk=Dv=128 conv width 4, "
+                      "bf16 in/out, fp32 state", "gdn_fork_08b_traffic.json"),
+}
+
+
+def bench_gdn_layer(a):
+    """One step = one state-fork GDN layer call: the conv kernel of both streams, then the fused fork."""
     import torch
 
     from dllm_qwen38_amd import gdn, inputs
 
+    shape_name, metric, workload, traffic_file = GDN_WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
-    s = inputs.GDN_27B_BF16
+    s = getattr(inputs, shape_name)
     x = inputs.gdn_layer_inputs(s)
     xd = {k: v.to(dev) for k, v in x.items()}
     plan = gdn.StateForkPlan(xd["raw0"], xd["rawt"], xd["conv_w"], xd["beta0"], xd["betat"], xd["g0"], xd["gt"],
                              num_k_heads=s.Hk, num_v_heads=s.Hv, head_k_dim=s.D, head_v_dim=s.D, block=s.block)
     stream = torch.cuda.current_stream(dev)
+    gdn.kernel_status(reset=True)
     for _ in range(a.warmup):
         plan.run()
     torch.cuda.synchronize(dev)
 
-    # timed region: K steps; events around each kernel on the launch stream
+    # timed region: K steps; HIP events around each kernel on the launch stream
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
     torch.cuda.synchronize(dev)
@@ -128,6 +165,11 @@ def main(argv=None):
         e2.record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
+    status = gdn.kernel_status(reset=True)
+    if status:
+        print(f"a bounded wait gave up during the timed steps (status {status}): the outputs are invalid",
+              file=sys.stderr)
+        return 1
     conv_ms = [e0.elapsed_time(e1) for e0, e1, _ in ev]
     core_ms = [e1.elapsed_time(e2) for _, e1, e2 in ev]
     step_ms = ev[0][0].elapsed_time(ev[-1][2]) / a.steps
@@ -135,14 +177,14 @@ def main(argv=None):
     core_avg = sum(core_ms) / len(core_ms)
     conv_avg = sum(conv_ms) / len(conv_ms)
 
-    Cd = s.conv_dim
-    T = s.B * s.L
+    # the fork kernel's algorithmic bytes: conv outputs of both streams read once, beta and g of
+    # both streams (fp32), both outputs, the fp32 state snapshots
+    Cd, T = s.conv_dim, s.B * s.L
     core_bytes = (2 * T * Cd * 2 + 2 * T * s.Hv * 8 + 2 * T * s.Hv * s.D * 2 + (T // s.block) * s.Hv * s.D * s.D * 4)
     core_flops = gdn.layer_flops(s.B, s.L, s.Hv, s.D, s.D, s.block)
     achieved = core_bytes / (core_avg * 1e-3) / 1e9
-    traffic = _traffic_from_profiles()
     res = {
-        "metric": "state-fork GDN layer tokens/s at 27B-class shape; % MFMA/HBM roofline",
+        "metric": metric,
         "value": tokens / (step_ms * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -154,12 +196,13 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) projections, sigmoid/softplus gates, U(-0.5,0.5) conv weight)",
-        "config": {"workload": "state-fork GDN layer, 27B-class: B=4 L=4096 block=chunk=32 Hk=16 Hv=48 "
-                               "Dk=Dv=128 conv width 4, bf16 in/out, fp32 state", "global_batch": s.B,
-                   "seq_len": s.L, "parallelism": "single GPU"},
+        "config": {"workload": workload, "global_batch": s.B, "seq_len": s.L, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(traffic_file),
+                     "kernel": "gdn_fork_pipe_kernel", "algorithmic_bytes": core_bytes},
         "kernels_ms": {"conv_fork": conv_avg, "gdn_state_fork": core_avg},
+        "layer_hbm": {"algorithmic_bytes": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block),
+                      "step_gbs": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block) / (step_ms * 1e-3) / 1e9},
         "mfma": {"kernel": "gdn_state_fork", "algorithmic_tflops": core_flops / (core_avg * 1e-3) / 1e12,
                  "peak_tflops": BF16_MFMA_PEAK_TFLOPS,
                  "frac": core_flops / (core_avg * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS},
@@ -174,7 +217,7 @@ def main(argv=None):
         torch.cuda.synchronize(dev)
         del src, dst
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(a.cpu_sample_L, a.cpu_budget_s)
+        res["cpu_baseline"] = cpu_baseline(s, min(a.cpu_sample_L, s.L), a.cpu_budget_s)
         res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
     print(json.dumps(res))
     return 0
@@ -247,7 +290,8 @@ def bench_attention(a):
         med = statistics.median(times)
         res["cpu_baseline"] = {"value": Ls / med, "unit": "tokens/s", "cores": n, "kind": "port",
                                "sample": f"B=1 L={Ls} (the first {Ls} positions of each half), same heads and d, "
-                                         f"fp32 torch CPU oracle; median of {len(times)} runs ({med:.2f} s/run)"}
+                                         f"fp32 torch CPU oracle; median of {len(times)} runs ({med:.2f} s/run)",
+                               **_host_info()}
     print(json.dumps(res))
     return 0
 

@@ -53,6 +53,8 @@ struct GdnArgs {
   int l2norm;
   int vec_qk;  // q/k rows: 16-byte vector loads (aligned, Dk equal to the kernel width)
   int vec_v;   // v rows: 16-byte vector loads (aligned, Dv a multiple of the column window)
+  int spin_limit;  // bounded waits give up (and report through dllm_status) after this many sleeps
+  int wait_bias;   // 0; tests set a count the LDS wait never reaches, to exercise the give-up path
 };
 
 // Linear workgroup id such that consecutive ids run on the same XCD (dispatch is round-robin over
@@ -823,6 +825,15 @@ enum { VS_EGQ = 0, VS_RNK = 32, VS_EGLK = 64, VS_EG = 96 };
 enum { VA_GAML = 0, VA_BET = 32, VA_EG = 64, VA_EGL = 96 };
 enum { VP_GAML = 0, VP_EG = 32 };
 
+// Bit of the library's per-device status word (dllm_status): the bounded LDS row-buffer wait of
+// the pipelined fork gave up (the launch's outputs are then invalid).
+enum { STATUS_LDS_WAIT = 1u };
+static __device__ unsigned dllm_status_word;
+
+__device__ __forceinline__ void report_status(unsigned bit) {
+  __hip_atomic_fetch_or(&dllm_status_word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   using SM = PipeSmem;
   using F = Frag<true>;
@@ -1185,9 +1196,13 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
       // tile; the wait is bounded, and they reach their raise without waiting on this wave)
       if (c + 1 < ntiles) put_rows(VB(gs, (c + 1) & 1), rv);
       if (c + 2 < ntiles) {
-        const unsigned target = 4u * (unsigned)(c + 1);
-        for (int spin = 0; spin < (1 << 22); ++spin) {
+        const unsigned target = 4u * (unsigned)(c + 1) + (unsigned)a.wait_bias;
+        for (int spin = 0;; ++spin) {
           if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+          if (spin >= a.spin_limit) {  // never expected: the state waves reach their raise unconditionally
+            if (lane == 0) report_status(STATUS_LDS_WAIT);
+            break;
+          }
           __builtin_amdgcn_s_sleep(1);
         }
         asm volatile("" ::: "memory");
@@ -1399,6 +1414,11 @@ static int dispatch_gdn(GdnArgs& a, int dtype, bool fork, hipStream_t st) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Sleeps after which a bounded wait gives up and sets a dllm_status bit (process-wide; tests lower
+// it to force that path).
+static int g_spin_limit = 1 << 20;
+static int g_wait_bias = 0;  // dllm_set_wait_test_mode
+
 static bool fits_i32(long long x) { return x >= -2147483647LL && x <= 2147483647LL; }
 
 }  // namespace dllm
@@ -1450,6 +1470,8 @@ extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const
   a.snap_every = chunk / a.sub;
   a.scale = scale;
   a.l2norm = use_qk_l2norm;
+  a.spin_limit = g_spin_limit;
+  a.wait_bias = g_wait_bias;
   const int esz = dtype == DT_BF16 ? 2 : 4;
   const int vel = 16 / esz;
   auto st_ok = [&](const int64_t* st3) { return (st3[0] % vel == 0) && (st3[1] % vel == 0) && (st3[2] % vel == 0); };
@@ -1501,6 +1523,8 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
   a.snap_every = 1;
   a.scale = scale;
   a.l2norm = 1;
+  a.spin_limit = g_spin_limit;
+  a.wait_bias = g_wait_bias;
   const int vel = 16 / esz;
   const bool st_ok = (qkv_stride_b % vel == 0) && (qkv_stride_t % vel == 0) && (Dk % vel == 0) && (Dv % vel == 0) &&
                      ((long long)Hk * Dk % vel == 0);
@@ -1510,4 +1534,31 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
   // full 128 x 128 heads with 16-byte rows: the pipelined kernel
   if (dtype == DT_BF16 && Dk == 128 && Dv == 128 && a.vec_qk && a.vec_v) return launch_fork_pipe(a, (hipStream_t)stream);
   return dispatch_gdn(a, dtype, true, (hipStream_t)stream);
+}
+
+extern "C" int dllm_set_spin_limit(int limit) {
+  if (limit < 0) return fail(DLLM_EINVAL, "spin limit %d < 0", limit);
+  const int prev = g_spin_limit;
+  g_spin_limit = limit;
+  return prev;
+}
+
+extern "C" int dllm_status(int reset) {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "dllm_status: %s", hipGetErrorString(e));
+  unsigned v = 0;
+  e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(dllm_status_word), sizeof(v), 0, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "dllm_status: %s", hipGetErrorString(e));
+  if (reset) {
+    const unsigned z = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(dllm_status_word), &z, sizeof(z), 0, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail(DLLM_ELAUNCH, "dllm_status: %s", hipGetErrorString(e));
+  }
+  return (int)(v & 0x7fffffffu);
+}
+
+extern "C" int dllm_set_wait_test_mode(int on) {
+  const int prev = g_wait_bias != 0;
+  g_wait_bias = on ? (1 << 30) : 0;
+  return prev;
 }

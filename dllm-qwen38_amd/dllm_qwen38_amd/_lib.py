@@ -35,6 +35,9 @@ _SIGNATURES = {
         _c_float, _c_void_p]),
     "dllm_gdn_fused_fork_supported": (_c_int, [_c_int, _c_int, _c_int]),
     "dllm_gdn_state_fork_path": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
+    "dllm_set_spin_limit": (_c_int, [_c_int]),
+    "dllm_status": (_c_int, [_c_int]),
+    "dllm_set_wait_test_mode": (_c_int, [_c_int]),
     "dllm_gdn_state_fork_fwd": (_c_int, [
         _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p, _c_fp, _c_fp, _c_void_p, _c_void_p,
         _c_fp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_void_p]),

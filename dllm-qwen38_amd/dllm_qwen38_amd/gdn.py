@@ -252,10 +252,12 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
             raise ValueError(f"{name} must be [B, L, Hv] = {(B, L, Hv)}")
     Lb = _lib.lib()
     sh = _lib.stream_handle(dev)
+    wcode = _lib.dtype_code(w.dtype)
+    cflags = 1 if fault == "no-conv-prefix" else 0
+    bias = None if conv_bias is None else conv_bias.contiguous()
     _lib.check(Lb.dllm_conv_fork_fwd(
-        r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(conv_bias), y0.data_ptr(), yt.data_ptr(),
-        _lib.ptr(tails), B, L, Cd, K, block, code, _lib.dtype_code(w.dtype), 1 if fault == "no-conv-prefix" else 0,
-        sh), "dllm_conv_fork_fwd")
+        r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(bias), y0.data_ptr(), yt.data_ptr(),
+        _lib.ptr(tails), B, L, Cd, K, block, code, wcode, cflags, sh), "dllm_conv_fork_fwd")
     if Lb.dllm_gdn_fused_fork_supported(Dk, block, code):
         _lib.check(Lb.dllm_gdn_state_fork_fwd(
             y0.data_ptr(), yt.data_ptr(), L * Cd, Cd, b0.data_ptr(), bt_.data_ptr(), gg0.data_ptr(), ggt.data_ptr(),
@@ -287,6 +289,16 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
 
 # kernel names reported through last_impl() for the fused fork (dllm_gdn_state_fork_path)
 _FORK_PATHS = {2: "pipelined fork kernel", 1: "fused fork kernel"}
+
+
+def kernel_status(reset: bool = True) -> int:
+    """Bits set by bounded waits inside kernels that gave up since the last reset (0 = none), after
+    a device synchronisation: 1 = the pipelined fork's LDS row-buffer wait. A set bit means the
+    launch that set it produced invalid outputs."""
+    st = _lib.lib().dllm_status(int(bool(reset)))
+    if st < 0:
+        raise RuntimeError(f"dllm_status failed: {_lib.last_error()}")
+    return st
 
 
 def fork_layout(B: int, L: int, block: int, width: int = 4, device="cuda"):

@@ -83,6 +83,22 @@ int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64_t qkv_stri
                             int Dv, int block, int dtype, float scale, void* stream);
 
 /*
+ * Bounded waits inside kernels (the pipelined fork's LDS row-buffer hand-off between its waves)
+ * give up after a limit and set a bit in a per-device status word instead of hanging:
+ * 1 = LDS row-buffer wait; a launch that set a bit produced invalid outputs.
+ * dllm_status synchronises the device and returns the bits of the current device (>= 0; reset != 0
+ * clears them). dllm_set_spin_limit sets the limit in sleeps (default 1 << 20, about 30-60 ms per
+ * wait; process-wide) and returns the previous one; tests lower it to exercise the reporting. No
+ * counterpart in the reference, whose CPU path has no such waits.
+ */
+int dllm_status(int reset);
+int dllm_set_spin_limit(int limit);
+/* Test only: with on != 0, the LDS row-buffer wait waits for a count that is never reached, so
+ * every such wait gives up after the spin limit (the kernel still ends, outputs invalid). Returns
+ * the previous mode. */
+int dllm_set_wait_test_mode(int on);
+
+/*
  * Causal depthwise conv + SiLU of both fork streams with conv-prefix carry-in.
  * Replaces [hf]:219-239 causal_conv1d_fn as called at src/dllm_qwen38/gdn.py:217-219 for the clean
  * stream and for the noised rows with the prefix cut at src/dllm_qwen38/blockdiff.py:167-173.

@@ -78,3 +78,10 @@ def test_fork_path_query():
     assert lib.dllm_gdn_state_fork_path(64, 64, 32, _lib.DT_BF16) == 1
     assert lib.dllm_gdn_state_fork_path(64, 64, 32, _lib.DT_F32) == 1
     assert lib.dllm_gdn_state_fork_path(128, 128, 64, _lib.DT_BF16) == 0
+
+
+def test_spin_limit_setter():
+    lib = _lib.lib()
+    assert lib.dllm_set_spin_limit(-1) == -1
+    prev = lib.dllm_set_spin_limit(1000)
+    assert lib.dllm_set_spin_limit(prev) == 1000

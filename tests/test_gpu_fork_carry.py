@@ -58,7 +58,7 @@ CARRY_SHAPES = [
 def test_pipe_fork_slow_decay_matches_oracle(dev, s):
     x = inputs.gdn_layer_inputs(s)
     r = _fork(s, x, dev)
-    assert gdn.last_impl() == ("hip", "pipelined fork kernel")
+    assert gdn.last_impl()[0] == "hip" and gdn.last_impl()[1].startswith("pipelined fork kernel")
     o0, ot, st, tails = _oracle(s, x)
     assert torch.equal(r["tails"], tails)
     assert st.abs().max().item() > 0.5, "the carried state must be non-negligible"
@@ -86,7 +86,7 @@ def test_pipe_fork_subtile_blocks(dev, block):
     s = _shape(f"Hk 4, Hv 8, block {block}", 2, 256, block, 4, 8, 4150 + block)
     x = inputs.gdn_layer_inputs(s)
     r = _fork(s, x, dev)
-    assert gdn.last_impl() == ("hip", "pipelined fork kernel")
+    assert gdn.last_impl()[0] == "hip" and gdn.last_impl()[1].startswith("pipelined fork kernel")
     o0, ot, st, tails = _oracle(s, x)
     assert torch.equal(r["tails"], tails)
     assert r["states"].shape == (2, 256 // block, 8, 128, 128)
@@ -102,7 +102,7 @@ def test_pipe_fork_need_states_false_is_bit_identical(dev):
     a = _fork(s, x, dev)
     b = _fork(s, x, dev, need_states=False, need_tails=False)
     assert b["states"] is None and b["tails"] is None
-    assert gdn.last_impl() == ("hip", "pipelined fork kernel")
+    assert gdn.last_impl()[0] == "hip" and gdn.last_impl()[1].startswith("pipelined fork kernel")
     assert torch.equal(a["o0"], b["o0"]) and torch.equal(a["ot"], b["ot"])
 
 

@@ -49,9 +49,17 @@ struct AttnArgs {
   int vec;            // 16-byte vector loads of q/k/v rows allowed
 };
 
-__device__ __forceinline__ int xcd_linear_id_attn(int bid, int n) {
-  const int q = n >> 3, r = n & 7, x = bid & 7, i = bid >> 3;
-  return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+// Work unit of dispatch slot bid among n. The dispatcher hands slot bid to XCD bid % 8, in order of
+// bid / 8 within an XCD. Units are numbered longest first, in chunks of `chunk` consecutive units
+// that read the same K/V head; chunk c runs on XCD c % 8, so that every XCD receives an equal share
+// of each length class (a contiguous range per XCD would give one XCD all the longest units) and a
+// K/V head's tiles are shared through that XCD's L2. Slots past the last whole row of eight chunks
+// map to themselves. A bijection of [0, n).
+__device__ __forceinline__ int attn_unit(int bid, int n, int chunk) {
+  const int full = n / (8 * chunk) * (8 * chunk);
+  if (bid >= full) return bid;
+  const int x = bid & 7, i = bid >> 3;
+  return ((i / chunk) * 8 + x) * chunk + i % chunk;
 }
 
 // visibility of key block kb of half kh from query block qb of half qh (0 = x_t, 1 = x_0)
@@ -115,8 +123,8 @@ __global__ __launch_bounds__(256) void bd_attn_kernel(AttnArgs a) {
   const int rep = a.Hq / a.Hkv;
 
   // work unit: longest first (tile group descending), then half, batch, KV head, query head in group
-  const int lin = xcd_linear_id_attn(blockIdx.x, gridDim.x);
   constexpr int NH = BC ? 1 : 2;  // query halves
+  const int lin = attn_unit(blockIdx.x, gridDim.x, NH * rep);
   const int per_g = NH * a.B * a.Hkv * rep;
   const int g = ng - 1 - lin / per_g;
   int rem = lin % per_g;
@@ -372,25 +380,6 @@ static int launch_attn(const AttnArgs& a, hipStream_t st) {
   return DLLM_OK;
 }
 
-// ---------------------------------------------------------------------------------------------
-// bf16, d == D in {64, 128, 256}: eight waves, two per 32-query tile. Both waves of a pair form
-// the whole S^T = K Q^T (lane = query) and take the same softmax decisions; wave e = 0 / 1 of the
-// pair accumulates d half e of O^T, so a wave holds all of Q but only half of O and the kernel
-// runs two waves per SIMD. (Splitting S between the pair instead needs an LDS exchange and a second
-// barrier per tile, which measured slower than computing S twice.)
-// K and V tiles travel global -> LDS by direct loads, no registers: each wave instruction moves
-// 1 KB = 64 lanes x 16 bytes; rows are dense with their 16-byte chunks XOR-swizzled (swz_key) so
-// that the K fragment reads and the V^T transpose reads are free of bank conflicts. A ring of NST
-// stages keeps NST - 1 tiles in flight ahead of the one being computed; one barrier per tile.
-// ---------------------------------------------------------------------------------------------
-template <int D>
-struct DmaSmem {
-  static constexpr int NST = 4;                  // ring stages
-  static constexpr int TILE_BYTES = 32 * D * 2;  // one K or V tile
-  static constexpr int STAGE = 2 * TILE_BYTES;   // K, then V
-  static constexpr int TOTAL = NST * STAGE;
-};
-
 // Chunk swizzle of a tile row: logical 16-byte chunk c of row r sits at physical chunk c ^ swz_key(r).
 // LDS has 64 banks of 4 bytes; a 16-byte read is served 16 lanes per pass and an 8-byte read 32
 // lanes per pass. The K fragment reads take one chunk of 16 consecutive rows per pass, so the key
@@ -418,26 +407,56 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// ---------------------------------------------------------------------------------------------
+// bf16, d == D in {64, 128, 256}: eight waves, a pair per 32-query tile, split by role.
+// Waves 0..3 (S waves) hold Q^T of query tile u = wave and form S^T = K Q^T (lane = query), the mask
+// and the online softmax for key tile n; they hand P (the B-operand fragment of P^T, lane-major) and
+// the rescale factor of each query to their partner through an LDS ring of two slots. Waves 4..7
+// (O waves) hold O^T of the same query tile over the whole d and, one key tile behind, apply the
+// rescale and accumulate O^T += V^T P^T. No product is formed twice, an S wave holds no O and an O
+// wave no Q, and each SIMD runs one wave of each kind. (A split of the pair by halves of d instead
+// forms S in both waves: measured 1.25x the time at d = 256.) The hand-off needs no extra
+// synchronisation: slot n % 2 is written in the phase of tile n and read in the phase of tile
+// n + 1, across the one barrier per tile.
+// K and V tiles travel global -> LDS by direct loads, no registers: each wave instruction moves
+// 1 KB = 64 lanes x 16 bytes; rows are dense with their 16-byte chunks XOR-swizzled (swz_key) so
+// that the K fragment reads and the V^T transpose reads are free of bank conflicts. A ring of four
+// stages is filled two tiles ahead (V of tile n - 1 stays in the ring while it is read).
+// ---------------------------------------------------------------------------------------------
+template <int D>
+struct SpSmem {
+  static constexpr int NST = 4;                  // K/V ring stages
+  static constexpr int TILE_BYTES = 32 * D * 2;
+  static constexpr int STAGE = 2 * TILE_BYTES;   // K, then V
+  // hand-off slot: P fragment (lo halves of the 64 lanes, then hi halves), rescale factor per
+  // lane, final running max and sum per lane, flags
+  static constexpr int P_LO = 0, P_HI = 1024, ALPHA = 2048, MFIN = 2304, LFIN = 2560, FLAGS = 2816;
+  static constexpr int SLOT = 2832;
+  static constexpr int O_SLOTS = NST * STAGE;
+  static constexpr int TOTAL = O_SLOTS + 4 * 2 * SLOT;  // [pair][parity]
+};
+enum { SP_SKIP = 1, SP_RESCALE = 2 };
+
 template <int D, bool BC>
-__global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
-  using SM = DmaSmem<D>;
+__global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
+  using SM = SpSmem<D>;
   using F = Frag<true>;
   typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
   constexpr int NST = SM::NST;
   constexpr int CH = D / 8;          // 16-byte chunks per row
   constexpr int DT = D / 32;         // 32-wide slices of d
-  constexpr int DH = D / 2;          // this wave's half of d for O
-  constexpr int SH = DH / 32;
   constexpr int RPI = 64 / CH;       // rows per 1 KB wave instruction
   constexpr int IPT = 32 / RPI;      // wave instructions per K (or V) tile
   constexpr int IPW = 2 * IPT / 8;   // per wave per tile
   static_assert(IPW >= 1 && (2 * IPT) % 8 == 0, "tile must split evenly over eight waves");
+  static_assert(SM::TOTAL <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, h = lane >> 5, l32 = lane & 31;
-  const int pair = wave >> 1, e = wave & 1;
+  const int pair = wave & 3;
+  const bool swave = wave < 4;
   const int L = a.L, C = a.C;
   const int Lq = BC ? a.M : L;
   const int Lk = BC ? a.N : L;
@@ -446,8 +465,9 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   const int ng = (ntq + 3) >> 2;
   const int rep = a.Hq / a.Hkv;
 
-  const int lin = xcd_linear_id_attn(blockIdx.x, gridDim.x);
+  // work unit: longest first (tile group descending), then half, batch, KV head, query head in group
   constexpr int NH = BC ? 1 : 2;
+  const int lin = attn_unit(blockIdx.x, gridDim.x, NH * rep);
   const int per_g = NH * a.B * a.Hkv * rep;
   const int g = ng - 1 - lin / per_g;
   int rem = lin % per_g;
@@ -484,8 +504,6 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
     if (n < n1) { kh = 1; j0 = (t1lo + n) * 32; }
     else { kh = 0; j0 = (t0lo + n - n1) * 32; }
   };
-  // key tiles of this workgroup: all of them, or (block-causal with a key split) one contiguous
-  // share; the shares' partial results are merged by attn_combine_kernel
   int nbeg = 0, nend = ntiles;
   if constexpr (BC) {
     if (a.ksplit > 1) {
@@ -499,158 +517,199 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
   const bf16* const kbase = (const bf16*)a.k + b * a.k_sb + (long long)hkv * a.k_sh;
   const bf16* const vbase = (const bf16*)a.v + b * a.v_sb + (long long)hkv * a.v_sh;
 
-  // Q^T fragments (lane = query), kept in registers. S contracts over d, and neither operand of
-  // K Q^T is an accumulator, so both use contiguous d runs: the first MFMA of slice s takes
-  // d = 32s + 8h .. +7, the second 32s + 16 + 8h .. +7 (16-byte loads, 16-byte LDS reads).
-  F qf[DT];
-  {
-    const int row = min(r0 + l32, Lq - 1);
-    const bf16* qp = qbase + (long long)((BC ? 0 : qh * L) + row) * a.q_st;
-#pragma unroll
-    for (int s = 0; s < DT; ++s) {
-      qf[s].lo = *(const bf16x8*)(qp + 32 * s + 8 * h);
-      qf[s].hi = *(const bf16x8*)(qp + 32 * s + 16 + 8 * h);
-    }
-  }
-  wait_vmcnt<0>();  // only the direct loads below are counted inside the loop
-
-  // direct global -> LDS staging of K and V tile n into its ring stage (this wave's IPW loads)
   auto stage_tile = [&](int n) {
     int kh, j0;
     tile_pos(n, kh, j0);
     unsigned char* const sb = smem + (n % NST) * SM::STAGE;
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
-      const int gi = wave * IPW + j;  // wave-uniform
+      const int gi = wave * IPW + j;
       const bool isv = gi >= IPT;
       const int row0 = (gi % IPT) * RPI;
       const int row = row0 + lane / CH;
       const int chunk = (lane % CH) ^ swz_key<D>(row);
-      const int key = min(j0 + row, Lk - 1);  // rows past the end load a valid row; they are masked
+      const int key = min(j0 + row, Lk - 1);
       const long long off = (long long)((BC ? 0 : kh * L) + key) * (isv ? a.v_st : a.k_st) + chunk * 8;
       const bf16* src = (isv ? vbase : kbase) + off;
       unsigned char* dst = sb + (isv ? SM::TILE_BYTES : 0) + row0 * (2 * D);
       dma_load16(src, dst);
     }
   };
-  // wait until tile n's loads (this wave's) have landed, given which later tiles were issued
-  auto wait_tile = [&](int n) {
-    const int ahead = min(NST - 2, nend - 1 - n);  // tiles issued after n and still allowed in flight
-    if (ahead >= 2) wait_vmcnt<2 * IPW>();
-    else if (ahead == 1) wait_vmcnt<IPW>();
-    else wait_vmcnt<0>();
+  // the first two tiles, then tile nbeg landed (the loop stages two tiles ahead)
+  auto prologue = [&]() {
+    if (nend > nbeg) {
+      stage_tile(nbeg);
+      if (nbeg + 1 < nend) stage_tile(nbeg + 1);
+      if (nbeg + 1 < nend) wait_vmcnt<IPW>();
+      else wait_vmcnt<0>();
+    }
+    __syncthreads();
   };
+  // end of the phase of tile n: tile n + 1's loads (this wave's) have landed, tile n + 2's may
+  // still travel; then the barrier (slot(n) written, tile n + 1 staged by every wave)
+  auto end_phase = [&](int n) {
+    if (n + 1 < nend) {
+      if (n + 2 < nend) wait_vmcnt<IPW>();
+      else wait_vmcnt<0>();
+    }
+    __syncthreads();
+  };
+  auto slot = [&](int n) { return smem + SM::O_SLOTS + (pair * 2 + (n & 1)) * SM::SLOT; };
 
-  f32x16 O[SH];
-#pragma unroll
-  for (int t = 0; t < SH; ++t) O[t] = zero16();
-  float mrow = -1e30f, lrow = 0.f;
-  static_assert(NST == 4, "wait_tile assumes up to two tiles in flight behind the waited one");
-
-#pragma unroll
-  for (int n = 0; n < NST - 1; ++n)
-    if (nbeg + n < nend) stage_tile(nbeg + n);
-  if (nend > nbeg) wait_tile(nbeg);
-  __syncthreads();
-  for (int n = nbeg; n < nend; ++n) {
-    if (n + NST - 1 < nend) stage_tile(n + NST - 1);  // its stage held tile n - 1, done before the barrier
-    int kh, j0;
-    tile_pos(n, kh, j0);
-    const int kb0 = j0 / C, kb1 = (min(Lk, j0 + 32) - 1) / C;
-    bool any = false, all = false;
-    if (wave_live) classify(qh, qb0, qb1, kh, kb0, kb1, a.leak, any, all);
-    const bool ragged = (j0 + 32 > Lk) || (r1 - r0 < 32);
-    const unsigned char* Ks = smem + (n % NST) * SM::STAGE;
-    const unsigned char* Vs = Ks + SM::TILE_BYTES;
-    if (any) {
-      // S^T = K Q^T: rows = keys (lane l32 reads key row l32), k = d
-      f32x16 st = zero16();
+  // The two roles run separate loops with the same barrier sequence, so that neither holds the
+  // other's registers (Q of the S waves, O of the O waves).
+  if (swave) {
+    // Q^T fragments of the query tile (contiguous d runs)
+    F qf[DT];
+    {
+      const int row = min(r0 + l32, Lq - 1);
+      const bf16* qp = qbase + (long long)((BC ? 0 : qh * L) + row) * a.q_st;
 #pragma unroll
       for (int s = 0; s < DT; ++s) {
-        F kf;
-        kf.lo = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 8 * h));
-        kf.hi = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 16 + 8 * h));
-        mma32(st, kf, qf[s]);
-      }
-      // issue order: the K fragments of two slices ahead of their products (four LDS reads in
-      // flight per wave instead of two)
-      if constexpr (DT >= 3) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
-#pragma unroll
-        for (int s = 0; s + 2 < DT; ++s) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
-      }
-#pragma unroll
-      for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;
-      if (!all || ragged) {
-        const int qi = r0 + l32;
-        const int qbl = (qa + qi) / C;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int kj = j0 + rho(v, h);
-          const bool okk = kj < Lk && qi < Lq && visible(qh, qbl, kh, kj / C, a.leak);
-          st[v] = okk ? st[v] : -INFINITY;
-        }
-      }
-      float mx = st[0];
-#pragma unroll
-      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, st[v]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // lazy rescale (see bd_attn_kernel)
-      constexpr float RESCALE_LOG2 = 8.f;
-      if (__builtin_amdgcn_ballot_w64(mx > mrow + RESCALE_LOG2) != 0) {
-        const float mnew = fmaxf(mrow, mx);
-        const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
-#pragma unroll
-        for (int t = 0; t < SH; ++t)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) O[t][v] *= alpha;
-        lrow *= alpha;
-        mrow = mnew;
-      }
-      float ps = 0.f;
-      f32x16 p;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        p[v] = __builtin_amdgcn_exp2f(st[v] - mrow);
-        ps += p[v];
-      }
-      ps += __shfl_xor(ps, 32);
-      lrow += ps;
-      F pf;
-      acc_to_frag(p, pf);
-      // O^T (this wave's d half) += V^T P^T; V^T fragments by transpose reads of the swizzled rows
-      const int sl = lane & 15;
-      const int krow = 4 * h + (sl >> 2);                      // + 8m
-      const int dcol = 16 * ((lane >> 4) & 1) + 4 * (sl & 3);  // + d0
-#pragma unroll
-      for (int t = 0; t < SH; ++t) {
-        const int d0 = e * DH + 32 * t;
-        bf16x4 r[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          r[m] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(Vs + swz_off<D>(8 * m + krow, d0 + dcol)));
-        F vf;
-        vf.lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
-        vf.hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
-        mma32(O[t], vf, pf);
+        qf[s].lo = *(const bf16x8*)(qp + 32 * s + 8 * h);
+        qf[s].hi = *(const bf16x8*)(qp + 32 * s + 16 + 8 * h);
       }
     }
-    if (n + 1 < nend) wait_tile(n + 1);
-    __syncthreads();  // tile n + 1 staged by every wave; every wave is done with tile n's stage
+    wait_vmcnt<0>();  // only the direct loads are counted inside the loop
+    float mrow = -1e30f, lrow = 0.f;  // running max (log2 units) and sum of the query
+    prologue();
+    for (int n = nbeg; n < nend; ++n) {
+      if (n + 2 < nend) stage_tile(n + 2);  // its stage held tile n - 2, done in the phase before
+      unsigned char* sl = slot(n);
+      int kh, j0;
+      tile_pos(n, kh, j0);
+      const int kb0 = j0 / C, kb1 = (min(Lk, j0 + 32) - 1) / C;
+      bool any = false, all = false;
+      if (wave_live) classify(qh, qb0, qb1, kh, kb0, kb1, a.leak, any, all);
+      int fl = SP_SKIP;
+      if (any) {
+        const bool ragged = (j0 + 32 > Lk) || (r1 - r0 < 32);
+        const unsigned char* Ks = smem + (n % NST) * SM::STAGE;
+        f32x16 st = zero16();
+#pragma unroll
+        for (int s = 0; s < DT; ++s) {
+          F kf;
+          kf.lo = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 8 * h));
+          kf.hi = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 16 + 8 * h));
+          mma32(st, kf, qf[s]);
+        }
+        if constexpr (DT >= 3) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
+#pragma unroll
+          for (int s = 0; s + 2 < DT; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;
+        if (!all || ragged) {
+          const int qi = r0 + l32;
+          const int qbl = (qa + qi) / C;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int kj = j0 + rho(v, h);
+            const bool okk = kj < Lk && qi < Lq && visible(qh, qbl, kh, kj / C, a.leak);
+            st[v] = okk ? st[v] : -INFINITY;
+          }
+        }
+        float mx = st[0];
+#pragma unroll
+        for (int v = 1; v < 16; ++v) mx = fmaxf(mx, st[v]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // lazy rescale (see bd_attn_kernel): the O wave applies alpha before adding this tile
+        constexpr float RESCALE_LOG2 = 8.f;
+        fl = 0;
+        if (__builtin_amdgcn_ballot_w64(mx > mrow + RESCALE_LOG2) != 0) {
+          const float mnew = fmaxf(mrow, mx);
+          const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+          *(float*)(sl + SM::ALPHA + 4 * lane) = alpha;
+          lrow *= alpha;
+          mrow = mnew;
+          fl = SP_RESCALE;
+        }
+        float ps = 0.f;
+        f32x16 p;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          p[v] = __builtin_amdgcn_exp2f(st[v] - mrow);
+          ps += p[v];
+        }
+        ps += __shfl_xor(ps, 32);
+        lrow += ps;
+        F pf;
+        acc_to_frag(p, pf);
+        *(bf16x8*)(sl + SM::P_LO + 16 * lane) = pf.lo;
+        *(bf16x8*)(sl + SM::P_HI + 16 * lane) = pf.hi;
+      }
+      if (lane == 0) *(int*)(sl + SM::FLAGS) = fl;
+      if (n == nend - 1) {  // the query's final max and sum travel with the last tile
+        *(float*)(sl + SM::MFIN + 4 * lane) = mrow;
+        *(float*)(sl + SM::LFIN + 4 * lane) = lrow;
+      }
+      end_phase(n);
+    }
+    return;
   }
 
+  // ---- O waves: O^T over the whole d (lane = query column), one tile behind
+  f32x16 O[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) O[t] = zero16();
+  // O^T += V^T P^T for the tile handed over in slot(n), after its rescale
+  auto o_step = [&](int n) {
+    const unsigned char* sl = slot(n);
+    const int fl = *(const int*)(sl + SM::FLAGS);
+    if (fl & SP_SKIP) return;
+    if (fl & SP_RESCALE) {
+      const float alpha = *(const float*)(sl + SM::ALPHA + 4 * lane);
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) O[t][v] *= alpha;
+    }
+    F pf;
+    pf.lo = *(const bf16x8*)(sl + SM::P_LO + 16 * lane);
+    pf.hi = *(const bf16x8*)(sl + SM::P_HI + 16 * lane);
+    const unsigned char* Vs = smem + (n % NST) * SM::STAGE + SM::TILE_BYTES;
+    const int sl4 = lane & 15;
+    const int krow = 4 * h + (sl4 >> 2);
+    const int dcol = 16 * ((lane >> 4) & 1) + 4 * (sl4 & 3);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      bf16x4 r[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        r[m] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(Vs + swz_off<D>(8 * m + krow, 32 * t + dcol)));
+      F vf;
+      vf.lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+      vf.hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
+      mma32(O[t], vf, pf);
+    }
+  };
+  prologue();
+  for (int n = nbeg; n < nend; ++n) {
+    if (n + 2 < nend) stage_tile(n + 2);
+    if (n > nbeg) o_step(n - 1);
+    end_phase(n);
+  }
+  if (nend > nbeg) o_step(nend - 1);
+
   const int qi = r0 + l32;
+  float mfin = -1e30f, lfin = 0.f;
+  if (nend > nbeg) {
+    const unsigned char* sl = slot(nend - 1);
+    mfin = *(const float*)(sl + SM::MFIN + 4 * lane);
+    lfin = *(const float*)(sl + SM::LFIN + 4 * lane);
+  }
   if constexpr (BC) {
-    if (a.ksplit > 1) {  // partial result of this key share, unnormalised
+    if (a.ksplit > 1) {  // partial result of this key share, unnormalised (an empty share: zeros)
       if (wave_live && qi < Lq) {
         const long long prow = (((long long)blockIdx.y * a.B + b) * Lq + qi) * a.Hq + hq;
-        float* op = a.opart + prow * D + e * DH;
+        float* op = a.opart + prow * D;
 #pragma unroll
-        for (int t = 0; t < SH; ++t)
+        for (int t = 0; t < DT; ++t)
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
             f32x4 o4;
@@ -658,20 +717,20 @@ __global__ __launch_bounds__(512) void bd_attn_dma_kernel(AttnArgs a) {
             for (int i = 0; i < 4; ++i) o4[i] = O[t][4 * m + i];
             *(f32x4*)(op + 32 * t + 8 * m + 4 * h) = o4;
           }
-        if (e == 0 && h == 0) {
-          a.mlpart[2 * prow] = mrow;
-          a.mlpart[2 * prow + 1] = lrow;
+        if (h == 0) {
+          a.mlpart[2 * prow] = mfin;
+          a.mlpart[2 * prow + 1] = lfin;
         }
       }
       return;
     }
   }
   if (wave_live && qi < Lq) {
-    const float inv = 1.f / lrow;
+    const float inv = 1.f / lfin;
     const long long orow = BC ? (long long)b * Lq + qi : (long long)b * 2 * L + qh * L + qi;
-    bf16* op = (bf16*)a.out + (orow * a.Hq + hq) * a.d + e * DH;
+    bf16* op = (bf16*)a.out + (orow * a.Hq + hq) * a.d;
 #pragma unroll
-    for (int t = 0; t < SH; ++t)
+    for (int t = 0; t < DT; ++t)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         bf16x4 o4;
@@ -712,13 +771,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 }
 
 template <int D, bool BC>
-static int launch_attn_dma(const AttnArgs& a, hipStream_t st) {
+static int launch_attn_sp(const AttnArgs& a, hipStream_t st) {
   const int ntq = ((BC ? a.M : a.L) + 31) / 32;
   const int ng = (ntq + 3) / 4;
   const long long nblk = (long long)ng * (BC ? 1 : 2) * a.B * a.Hq;
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "attention: grid too large");
   const int ks = BC && a.ksplit > 1 ? a.ksplit : 1;
-  bd_attn_dma_kernel<D, BC><<<dim3((unsigned)nblk, ks), dim3(512), 0, st>>>(a);
+  bd_attn_sp_kernel<D, BC><<<dim3((unsigned)nblk, ks), dim3(512), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention launch: %s", hipGetErrorString(e));
   if (ks > 1) {
@@ -749,9 +808,9 @@ static int dispatch_attn(AttnArgs& a, const int64_t* const sts[3], int dtype, hi
     // the direct-load kernel needs whole 16-byte rows of exactly d elements (vectorisable layout)
     if (vec && d == dw && dw >= 64 && (a.k_st % 8) == 0 && (a.v_st % 8) == 0) {
       switch (dw) {
-        case 64: return launch_attn_dma<64, BC>(a, st);
-        case 128: return launch_attn_dma<128, BC>(a, st);
-        default: return launch_attn_dma<256, BC>(a, st);
+        case 64: return launch_attn_sp<64, BC>(a, st);
+        case 128: return launch_attn_sp<128, BC>(a, st);
+        default: return launch_attn_sp<256, BC>(a, st);
       }
     }
     switch (dw) {

@@ -423,16 +423,30 @@ __device__ __forceinline__ void wait_vmcnt() {
 // that the K fragment reads and the V^T transpose reads are free of bank conflicts. A ring of four
 // stages is filled two tiles ahead (V of tile n - 1 stays in the ring while it is read).
 // ---------------------------------------------------------------------------------------------
+// Max / sum of lane l's value and lane l ^ 32's (the two rows of an MFMA accumulator column),
+// exchanged by the gfx950 lane swap between the wave halves instead of through LDS. The sum's
+// operands are those of x + shfl_xor(x, 32), so both give the same bits.
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int D>
 struct SpSmem {
-  static constexpr int NST = 4;                  // K/V ring stages
-  static constexpr int TILE_BYTES = 32 * D * 2;
-  static constexpr int STAGE = 2 * TILE_BYTES;   // K, then V
+  // K and V ring stages: four at d = 256 (one phase more of loads in flight, measured 4% faster),
+  // three below, where the smaller footprint lets two workgroups share a CU
+  static constexpr int NKS = D == 256 ? 4 : 3, NVS = NKS;
+  static constexpr int TILE_BYTES = 32 * D * 2;  // one K or V tile of 32 keys
+  static constexpr int K_RING = 0, V_RING = NKS * TILE_BYTES;
   // hand-off slot: P fragment (lo halves of the 64 lanes, then hi halves), rescale factor per
-  // lane, final running max and sum per lane, flags
+  // lane, running max and sum per lane, flags
   static constexpr int P_LO = 0, P_HI = 1024, ALPHA = 2048, MFIN = 2304, LFIN = 2560, FLAGS = 2816;
   static constexpr int SLOT = 2832;
-  static constexpr int O_SLOTS = NST * STAGE;
+  static constexpr int O_SLOTS = (NKS + NVS) * TILE_BYTES;
   static constexpr int TOTAL = O_SLOTS + 4 * 2 * SLOT;  // [pair][parity]
 };
 enum { SP_SKIP = 1, SP_RESCALE = 2 };
@@ -442,13 +456,12 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
   using SM = SpSmem<D>;
   using F = Frag<true>;
   typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-  constexpr int NST = SM::NST;
   constexpr int CH = D / 8;          // 16-byte chunks per row
   constexpr int DT = D / 32;         // 32-wide slices of d
   constexpr int RPI = 64 / CH;       // rows per 1 KB wave instruction
   constexpr int IPT = 32 / RPI;      // wave instructions per K (or V) tile
-  constexpr int IPW = 2 * IPT / 8;   // per wave per tile
-  static_assert(IPW >= 1 && (2 * IPT) % 8 == 0, "tile must split evenly over eight waves");
+  constexpr int LPW = IPT / 4;       // per wave per tile: the S waves load K, the O waves V
+  static_assert(LPW >= 1 && IPT % 4 == 0, "a tile's rows split over four waves");
   static_assert(SM::TOTAL <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(16))) unsigned char smem[SM::TOTAL];
 
@@ -517,45 +530,44 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
   const bf16* const kbase = (const bf16*)a.k + b * a.k_sb + (long long)hkv * a.k_sh;
   const bf16* const vbase = (const bf16*)a.v + b * a.v_sb + (long long)hkv * a.v_sh;
 
-  auto stage_tile = [&](int n) {
+  // Direct load j of this wave's LPW for tile m (K rows by an S wave, V rows by an O wave) into
+  // the tile's ring stage. A CU keeps about 32 such 1 KB loads in flight and one wave issues one
+  // about every 100-140 cycles (measured), so all eight waves share a tile's loads: the S waves
+  // at the start of the phase, the O waves between their products.
+  auto stage_one = [&](int m, int j) {
     int kh, j0;
-    tile_pos(n, kh, j0);
-    unsigned char* const sb = smem + (n % NST) * SM::STAGE;
+    tile_pos(m, kh, j0);
+    const int row0 = (pair * LPW + j) * RPI;
+    const int row = row0 + lane / CH;
+    const int chunk = (lane % CH) ^ swz_key<D>(row);
+    const int key = min(j0 + row, Lk - 1);
+    const long long off = (long long)((BC ? 0 : kh * L) + key) * (swave ? a.k_st : a.v_st) + chunk * 8;
+    const bf16* src = (swave ? kbase : vbase) + off;
+    unsigned char* dst = smem + (swave ? SM::K_RING + (m % SM::NKS) * SM::TILE_BYTES
+                                       : SM::V_RING + (m % SM::NVS) * SM::TILE_BYTES) + row0 * (2 * D);
+    dma_load16(src, dst);
+  };
+  auto stage_tile = [&](int m) {
+    if (m < nend)
 #pragma unroll
-    for (int j = 0; j < IPW; ++j) {
-      const int gi = wave * IPW + j;
-      const bool isv = gi >= IPT;
-      const int row0 = (gi % IPT) * RPI;
-      const int row = row0 + lane / CH;
-      const int chunk = (lane % CH) ^ swz_key<D>(row);
-      const int key = min(j0 + row, Lk - 1);
-      const long long off = (long long)((BC ? 0 : kh * L) + key) * (isv ? a.v_st : a.k_st) + chunk * 8;
-      const bf16* src = (isv ? vbase : kbase) + off;
-      unsigned char* dst = sb + (isv ? SM::TILE_BYTES : 0) + row0 * (2 * D);
-      dma_load16(src, dst);
-    }
-  };
-  // the first two tiles, then tile nbeg landed (the loop stages two tiles ahead)
-  auto prologue = [&]() {
-    if (nend > nbeg) {
-      stage_tile(nbeg);
-      if (nbeg + 1 < nend) stage_tile(nbeg + 1);
-      if (nbeg + 1 < nend) wait_vmcnt<IPW>();
-      else wait_vmcnt<0>();
-    }
-    __syncthreads();
-  };
-  // end of the phase of tile n: tile n + 1's loads (this wave's) have landed, tile n + 2's may
-  // still travel; then the barrier (slot(n) written, tile n + 1 staged by every wave)
-  auto end_phase = [&](int n) {
-    if (n + 1 < nend) {
-      if (n + 2 < nend) wait_vmcnt<IPW>();
-      else wait_vmcnt<0>();
-    }
-    __syncthreads();
+      for (int j = 0; j < LPW; ++j) stage_one(m, j);
   };
   auto slot = [&](int n) { return smem + SM::O_SLOTS + (pair * 2 + (n & 1)) * SM::SLOT; };
+  constexpr int KD = SM::NKS, VD = SM::NVS - 2;  // load distances of K and V in phases
+  static_assert(KD >= 3 && KD <= 4 && VD >= 1 && VD <= 2, "stage counts");
+  // wait until at most `tiles` of this wave's tile loads are still in flight
+  auto wait_tiles = [&](int tiles) {
+    if (tiles >= 2) wait_vmcnt<2 * LPW>();
+    else if (tiles == 1) wait_vmcnt<LPW>();
+    else wait_vmcnt<0>();
+  };
 
+  // Schedule (phase n = the barrier interval of tile n): the S waves form S^T of tile n + 1 and,
+  // in the same instruction stream, the softmax of tile n (formed in the phase before), so that
+  // the products of one run in the matrix core while the vector unit works on the other; the O
+  // waves accumulate tile n - 1. K of tile m is loaded in phase m - KD and read in phase m - 1, V
+  // of tile m is loaded in phase m - VD and read in phase m + 1: each stage is reloaded in the
+  // phase after its last read.
   // The two roles run separate loops with the same barrier sequence, so that neither holds the
   // other's registers (Q of the S waves, O of the O waves).
   if (swave) {
@@ -570,85 +582,103 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
         qf[s].hi = *(const bf16x8*)(qp + 32 * s + 16 + 8 * h);
       }
     }
-    wait_vmcnt<0>();  // only the direct loads are counted inside the loop
+    // keys visible to this lane's query in each half: [vlo, vhi) (empty past the last query)
+    const int qi = r0 + l32;
+    const int qbl = (qa + qi) / C;
+    int vlo0, vhi0, vlo1, vhi1;
+    if (qh == 1) {
+      vlo0 = vhi0 = 0;
+      vlo1 = 0;
+      vhi1 = min(Lk, (qbl + 1) * C);
+    } else {
+      vlo0 = a.leak ? 0 : qbl * C;
+      vhi0 = min(Lk, (qbl + 1) * C);
+      vlo1 = 0;
+      vhi1 = min(Lk, qbl * C);
+    }
+    if (!(wave_live && qi < Lq)) vhi0 = vlo0, vhi1 = vlo1;
     float mrow = -1e30f, lrow = 0.f;  // running max (log2 units) and sum of the query
-    prologue();
-    for (int n = nbeg; n < nend; ++n) {
-      if (n + 2 < nend) stage_tile(n + 2);  // its stage held tile n - 2, done in the phase before
-      unsigned char* sl = slot(n);
+
+    auto s_product = [&](int m) {  // S^T = K Q^T of tile m (its K stage)
+      const unsigned char* Ks = smem + SM::K_RING + (m % SM::NKS) * SM::TILE_BYTES;
+      f32x16 st = zero16();
+#pragma unroll
+      for (int s = 0; s < DT; ++s) {
+        F kf;
+        kf.lo = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 8 * h));
+        kf.hi = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 16 + 8 * h));
+        mma32(st, kf, qf[s]);
+      }
+      return st;
+    };
+    // phase n: cur holds S^T of tile n; nxt receives S^T of tile n + 1
+    auto s_phase = [&](int n, f32x16& cur, f32x16& nxt) {
+      stage_tile(n + KD);  // its stage held K of tile n, read in the phase before
       int kh, j0;
       tile_pos(n, kh, j0);
       const int kb0 = j0 / C, kb1 = (min(Lk, j0 + 32) - 1) / C;
       bool any = false, all = false;
       if (wave_live) classify(qh, qb0, qb1, kh, kb0, kb1, a.leak, any, all);
-      int fl = SP_SKIP;
-      if (any) {
-        const bool ragged = (j0 + 32 > Lk) || (r1 - r0 < 32);
-        const unsigned char* Ks = smem + (n % NST) * SM::STAGE;
-        f32x16 st = zero16();
-#pragma unroll
-        for (int s = 0; s < DT; ++s) {
-          F kf;
-          kf.lo = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 8 * h));
-          kf.hi = *(const bf16x8*)(Ks + swz_off<D>(l32, 32 * s + 16 + 8 * h));
-          mma32(st, kf, qf[s]);
-        }
-        if constexpr (DT >= 3) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
-#pragma unroll
-          for (int s = 0; s + 2 < DT; ++s) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
-          }
-          __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
-        }
-#pragma unroll
-        for (int v = 0; v < 16; ++v) st[v] *= a.scale_log2e;
-        if (!all || ragged) {
-          const int qi = r0 + l32;
-          const int qbl = (qa + qi) / C;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int kj = j0 + rho(v, h);
-            const bool okk = kj < Lk && qi < Lq && visible(qh, qbl, kh, kj / C, a.leak);
-            st[v] = okk ? st[v] : -INFINITY;
-          }
-        }
-        float mx = st[0];
-#pragma unroll
-        for (int v = 1; v < 16; ++v) mx = fmaxf(mx, st[v]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // lazy rescale (see bd_attn_kernel): the O wave applies alpha before adding this tile
-        constexpr float RESCALE_LOG2 = 8.f;
-        fl = 0;
-        if (__builtin_amdgcn_ballot_w64(mx > mrow + RESCALE_LOG2) != 0) {
-          const float mnew = fmaxf(mrow, mx);
-          const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
-          *(float*)(sl + SM::ALPHA + 4 * lane) = alpha;
-          lrow *= alpha;
-          mrow = mnew;
-          fl = SP_RESCALE;
-        }
-        float ps = 0.f;
-        f32x16 p;
+      const bool ragged = (j0 + 32 > Lk) || (r1 - r0 < 32);
+      if (!all || ragged) {  // keys this lane's query may not see -> -inf (a tile none may see: all)
+        const int lo = kh ? vlo1 : vlo0, hi = kh ? vhi1 : vhi0;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          p[v] = __builtin_amdgcn_exp2f(st[v] - mrow);
-          ps += p[v];
+          const int kj = j0 + rho(v, h);
+          cur[v] = (kj >= lo && kj < hi) ? cur[v] : -INFINITY;
         }
-        ps += __shfl_xor(ps, 32);
-        lrow += ps;
-        F pf;
-        acc_to_frag(p, pf);
-        *(bf16x8*)(sl + SM::P_LO + 16 * lane) = pf.lo;
-        *(bf16x8*)(sl + SM::P_HI + 16 * lane) = pf.hi;
       }
-      if (lane == 0) *(int*)(sl + SM::FLAGS) = fl;
-      if (n == nend - 1) {  // the query's final max and sum travel with the last tile
-        *(float*)(sl + SM::MFIN + 4 * lane) = mrow;
-        *(float*)(sl + SM::LFIN + 4 * lane) = lrow;
+      // S^T of tile n + 1 (past the last tile: a stale stage, never used)
+      nxt = s_product(n + 1);
+      // softmax of tile n, branch-free so that it interleaves with the products above; scores in
+      // log2 units, the exponent formed with one rounding (fma of the raw score)
+      const float sc = a.scale_log2e;
+      float mx = cur[0] * sc;
+#pragma unroll
+      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, cur[v] * sc);
+      mx = halves_max(mx);
+      // lazy rescale (see bd_attn_kernel): the O wave applies alpha before adding this tile;
+      // without a rescale alpha = 1 (selected: the hardware 2^0 need not be exactly 1)
+      constexpr float RESCALE_LOG2 = 8.f;
+      const bool resc = __builtin_amdgcn_ballot_w64(mx > mrow + RESCALE_LOG2) != 0;
+      const float mnew = resc ? fmaxf(mrow, mx) : mrow;
+      const float alpha = resc ? __builtin_amdgcn_exp2f(mrow - mnew) : 1.f;
+      lrow *= alpha;
+      mrow = mnew;
+      float ps = 0.f;
+      f32x16 p;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[v], sc, -mrow));
+        ps += p[v];
       }
-      end_phase(n);
+      ps = halves_sum(ps);
+      lrow += ps;
+      F pf;
+      acc_to_frag(p, pf);
+      unsigned char* sl = slot(n);
+      *(bf16x8*)(sl + SM::P_LO + 16 * lane) = pf.lo;
+      *(bf16x8*)(sl + SM::P_HI + 16 * lane) = pf.hi;
+      *(float*)(sl + SM::ALPHA + 4 * lane) = alpha;
+      *(float*)(sl + SM::MFIN + 4 * lane) = mrow;  // the last tile's carry the final max and sum
+      *(float*)(sl + SM::LFIN + 4 * lane) = lrow;
+      *(int*)(sl + SM::FLAGS) = any ? (resc ? SP_RESCALE : 0) : SP_SKIP;  // every lane: one value
+      // end of the phase: K of tile n + 2 landed (n + 3 .. n + KD may travel), then the barrier
+      wait_tiles(min(KD - 2, max(0, nend - (n + 3))));
+      __syncthreads();
+    };
+
+    // prologue: K of the first KD tiles, the first two landed; S^T of the first tile
+    wait_vmcnt<0>();  // only the direct loads are counted below
+#pragma unroll
+    for (int i = 0; i < KD; ++i) stage_tile(nbeg + i);
+    wait_tiles(min(KD - 2, max(0, nend - (nbeg + 2))));
+    __syncthreads();
+    f32x16 sa = s_product(nbeg), sb;  // past the last tile: never used
+    __syncthreads();  // the first phase restages K of tile nbeg's stage
+    for (int n = nbeg; n < nend; n += 2) {
+      s_phase(n, sa, sb);
+      if (n + 1 < nend) s_phase(n + 1, sb, sa);
     }
     return;
   }
@@ -657,44 +687,66 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
   f32x16 O[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) O[t] = zero16();
-  // O^T += V^T P^T for the tile handed over in slot(n), after its rescale
-  auto o_step = [&](int n) {
-    const unsigned char* sl = slot(n);
-    const int fl = *(const int*)(sl + SM::FLAGS);
-    if (fl & SP_SKIP) return;
+  // One phase of an O wave: O^T += V^T P^T for the tile handed over in slot(m) (m < 0: none),
+  // after its rescale, with this wave's direct loads of V tile sv (past the last: none) between
+  // the d slices.
+  auto o_phase = [&](int m, int sv) {
+    int fl = SP_SKIP;
+    F pf;
+    float alpha = 1.f;
+    if (m >= 0) {  // the slot's words are read together (P and alpha are unused when skipped)
+      const unsigned char* sl = slot(m);
+      fl = *(const int*)(sl + SM::FLAGS);
+      pf.lo = *(const bf16x8*)(sl + SM::P_LO + 16 * lane);
+      pf.hi = *(const bf16x8*)(sl + SM::P_HI + 16 * lane);
+      alpha = *(const float*)(sl + SM::ALPHA + 4 * lane);
+    }
+    if (fl & SP_SKIP) {
+      stage_tile(sv);
+      return;
+    }
     if (fl & SP_RESCALE) {
-      const float alpha = *(const float*)(sl + SM::ALPHA + 4 * lane);
 #pragma unroll
       for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int v = 0; v < 16; ++v) O[t][v] *= alpha;
     }
-    F pf;
-    pf.lo = *(const bf16x8*)(sl + SM::P_LO + 16 * lane);
-    pf.hi = *(const bf16x8*)(sl + SM::P_HI + 16 * lane);
-    const unsigned char* Vs = smem + (n % NST) * SM::STAGE + SM::TILE_BYTES;
+    const unsigned char* Vs = smem + SM::V_RING + (m % SM::NVS) * SM::TILE_BYTES;
     const int sl4 = lane & 15;
     const int krow = 4 * h + (sl4 >> 2);
     const int dcol = 16 * ((lane >> 4) & 1) + 4 * (sl4 & 3);
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
+    F vf[DT];
+    auto vread = [&](int t) {
       bf16x4 r[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        r[m] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(Vs + swz_off<D>(8 * m + krow, 32 * t + dcol)));
-      F vf;
-      vf.lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
-      vf.hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
-      mma32(O[t], vf, pf);
+      for (int q = 0; q < 4; ++q)
+        r[q] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(Vs + swz_off<D>(8 * q + krow, 32 * t + dcol)));
+      vf[t].lo = __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7);
+      vf[t].hi = __builtin_shufflevector(r[2], r[3], 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    constexpr int AHEAD = DT < 3 ? DT : 3;  // V^T fragments in flight ahead of the product
+#pragma unroll
+    for (int t = 0; t < AHEAD; ++t) vread(t);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      if (t + AHEAD < DT) vread(t + AHEAD);
+      mma32(O[t], vf[t], pf);
+      if (sv < nend && ((t + 1) * LPW) / DT != (t * LPW) / DT) stage_one(sv, (t * LPW) / DT);
     }
   };
-  prologue();
+  // prologue: V of the first VD tiles; the S waves' two barriers
+#pragma unroll
+  for (int i = 0; i < VD; ++i) stage_tile(nbeg + i);
+  __syncthreads();
+  __syncthreads();
   for (int n = nbeg; n < nend; ++n) {
-    if (n + 2 < nend) stage_tile(n + 2);
-    if (n > nbeg) o_step(n - 1);
-    end_phase(n);
+    // V stage of tile n + VD held tile n - 2, read in the phase before
+    o_phase(n > nbeg ? n - 1 : -1, n + VD);
+    // end of the phase: V of tile n landed (n + 1 .. n + VD may travel), then the barrier
+    wait_tiles(min(VD, max(0, nend - (n + 1))));
+    __syncthreads();
   }
-  if (nend > nbeg) o_step(nend - 1);
+  if (nend > nbeg) o_phase(nend - 1, nend);
 
   const int qi = r0 + l32;
   float mfin = -1e30f, lfin = 0.f;

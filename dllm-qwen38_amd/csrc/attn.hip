@@ -632,11 +632,11 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
       nxt = s_product(n + 1);
       // softmax of tile n, branch-free so that it interleaves with the products above; scores in
       // log2 units, the exponent formed with one rounding (fma of the raw score)
-      const float sc = a.scale_log2e;
-      float mx = cur[0] * sc;
+      const float sc = a.scale_log2e;  // > 0 (dispatch): the max of the rounded products is the
+      float mx = cur[0];               // rounded product of the max
 #pragma unroll
-      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, cur[v] * sc);
-      mx = halves_max(mx);
+      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, cur[v]);
+      mx = halves_max(mx) * sc;
       // lazy rescale (see bd_attn_kernel): the O wave applies alpha before adding this tile;
       // without a rescale alpha = 1 (selected: the hardware 2^0 need not be exactly 1)
       constexpr float RESCALE_LOG2 = 8.f;
@@ -858,7 +858,9 @@ static int dispatch_attn(AttnArgs& a, const int64_t* const sts[3], int dtype, hi
   a.vec = vec;
   if (dtype == DT_BF16) {
     // the direct-load kernel needs whole 16-byte rows of exactly d elements (vectorisable layout)
-    if (vec && d == dw && dw >= 64 && (a.k_st % 8) == 0 && (a.v_st % 8) == 0) {
+    // and a positive finite softmax scale
+    if (vec && d == dw && dw >= 64 && (a.k_st % 8) == 0 && (a.v_st % 8) == 0 && a.scale_log2e > 0.f &&
+        a.scale_log2e < INFINITY) {
       switch (dw) {
         case 64: return launch_attn_sp<64, BC>(a, st);
         case 128: return launch_attn_sp<128, BC>(a, st);

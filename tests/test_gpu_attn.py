@@ -51,6 +51,17 @@ def test_bd_attention_matches_oracle(dev, dtype, B, L, Hq, Hkv, d, block):
     _check(got, ref, dtype, f"{dtype} B{B} L{L} Hq{Hq} Hkv{Hkv} d{d} block{block}", v.float().abs().max().item())
 
 
+@pytest.mark.parametrize("scale", [0.2, -0.05, 0.0])
+def test_custom_scales(dev, scale):
+    """A positive scale runs the bf16 direct-load kernel (its softmax max is taken over the raw
+    scores and scaled once, which needs scale > 0); zero or negative scales run the general kernel."""
+    q, k, v = _inputs(1, 128, 4, 2, 128, torch.bfloat16, seed=77)
+    got = attention.bd_attention(q.to(dev), k.to(dev), v.to(dev), block=32, scale=scale)
+    torch.cuda.synchronize()
+    ref = attn_ref.bd_attention(q, k, v, block=32, scale=scale)
+    _check(got, ref, torch.bfloat16, f"scale {scale}", v.float().abs().max().item())
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_mask_leak_fault_matches_oracle_and_differs(dev, dtype):
     q, k, v = _inputs(1, 64, 4, 2, 64, dtype, seed=5)

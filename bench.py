@@ -74,13 +74,17 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--cpu-sample-L", type=int, default=4096)
     ap.add_argument("--cpu-budget-s", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibration-copy-gib", type=float, default=0.0,
                     help="after the timed steps, copy this many GiB device-to-device (the reference transfer "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--pieces", type=int, default=None,
+                    help="GDN layer workloads: the step's schedule, the layer cut into this many block ranges "
+                         "with the conv of each range beside the fork of the one before (1 = conv, then fork; "
+                         "default 4 at the 27B-class shape, 1 at the 0.8B-class shape, where it measured no gain)")
     ap.add_argument("--workload", default="gdn-layer",
                     choices=["gdn-layer", "gdn-layer-08b", "attention", "stack", "decode"],
                     help="gdn-layer (default, the headline metric); gdn-layer-08b: the same layer at the 0.8B-class "
@@ -126,20 +130,23 @@ def _host_info():
 GDN_WORKLOADS = {
     "gdn-layer": ("GDN_27B_BF16", "state-fork GDN layer tokens/s at 27B-class shape; % MFMA/HBM roofline",
                   "state-fork GDN layer, 27B-class: B=4 L=4096 block=chunk=32 Hk=16 Hv=48 Dk=Dv=128 conv width 4, "
-                  "bf16 in/out, fp32 state", "gdn_fork_27b_traffic.json"),
+                  "bf16 in/out, fp32 state", "gdn_fork_27b_traffic.json", 4),
     "gdn-layer-08b": ("GDN_08B_BF16", "state-fork GDN layer tokens/s at 0.8B-class shape; % MFMA/HBM roofline",
                       "state-fork GDN layer, 0.8B-class: B=8 L=2048 block=chunk=32 Hk=Hv=16 Dk=Dv=128 conv width 4, "
-                      "bf16 in/out, fp32 state", "gdn_fork_08b_traffic.json"),
+                      "bf16 in/out, fp32 state", "gdn_fork_08b_traffic.json", 1),
 }
 
 
 def bench_gdn_layer(a):
-    """One step = one state-fork GDN layer call: the conv kernel of both streams, then the fused fork."""
+    """One step = one state-fork GDN layer call: the conv of both streams and the fused fork. With
+    pieces > 1 the step is StateForkPlan.run_overlapped (the conv of each block range beside the
+    fork of the range before; bit-identical results). The per-kernel roofline comes from a second
+    pass of the two kernels back to back, each between HIP events."""
     import torch
 
     from dllm_qwen38_amd import gdn, inputs
 
-    shape_name, metric, workload, traffic_file = GDN_WORKLOADS[a.workload]
+    shape_name, metric, workload, traffic_file, default_pieces = GDN_WORKLOADS[a.workload]
     dev = torch.device("cuda:0")
     s = getattr(inputs, shape_name)
     x = inputs.gdn_layer_inputs(s)
@@ -147,16 +154,31 @@ def bench_gdn_layer(a):
     plan = gdn.StateForkPlan(xd["raw0"], xd["rawt"], xd["conv_w"], xd["beta0"], xd["betat"], xd["g0"], xd["gt"],
                              num_k_heads=s.Hk, num_v_heads=s.Hv, head_k_dim=s.D, head_v_dim=s.D, block=s.block)
     stream = torch.cuda.current_stream(dev)
+    pieces = default_pieces if a.pieces is None else max(1, a.pieces)
+    if pieces > 1 and not plan.overlap_supported():
+        pieces = 1
+    step = (lambda: plan.run_overlapped(pieces)) if pieces > 1 else plan.run
     gdn.kernel_status(reset=True)
     for _ in range(a.warmup):
-        plan.run()
+        step()
     torch.cuda.synchronize(dev)
 
-    # timed region: K steps; HIP events around each kernel on the launch stream
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
+    # timed region: K steps of the schedule between HIP events on the launch stream (the side
+    # stream's conv ranges join it through events before its last fork range)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
+    s0.record(stream)
+    for _ in range(a.steps):
+        step()
+    s1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    step_ms = s0.elapsed_time(s1) / a.steps
+
+    # kernels alone: the same K steps as conv, then fork, with HIP events around each kernel
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
     for e0, e1, e2 in ev:
         e0.record(stream)
         plan.run_conv()
@@ -164,7 +186,6 @@ def bench_gdn_layer(a):
         plan.run_core()
         e2.record(stream)
     torch.cuda.synchronize(dev)
-    wall = time.perf_counter() - t0
     status = gdn.kernel_status(reset=True)
     if status:
         print(f"a bounded wait gave up during the timed steps (status {status}): the outputs are invalid",
@@ -172,7 +193,7 @@ def bench_gdn_layer(a):
         return 1
     conv_ms = [e0.elapsed_time(e1) for e0, e1, _ in ev]
     core_ms = [e1.elapsed_time(e2) for _, e1, e2 in ev]
-    step_ms = ev[0][0].elapsed_time(ev[-1][2]) / a.steps
+    seq_step_ms = ev[0][0].elapsed_time(ev[-1][2]) / a.steps
     tokens = s.B * s.L
     core_avg = sum(core_ms) / len(core_ms)
     conv_avg = sum(conv_ms) / len(conv_ms)
@@ -201,6 +222,7 @@ def bench_gdn_layer(a):
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(traffic_file),
                      "kernel": "gdn_fork_pipe_kernel", "algorithmic_bytes": core_bytes},
         "kernels_ms": {"conv_fork": conv_avg, "gdn_state_fork": core_avg},
+        "schedule": {"pieces": pieces, "ms_per_step_conv_then_fork": seq_step_ms},
         "layer_hbm": {"algorithmic_bytes": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block),
                       "step_gbs": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block) / (step_ms * 1e-3) / 1e9},
         "mfma": {"kernel": "gdn_state_fork", "algorithmic_tflops": core_flops / (core_avg * 1e-3) / 1e12,

@@ -27,12 +27,12 @@ template <typename TX, typename TW, int K, int VEC, int BLK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BLK > 0 ? 5 : 1, BLK > 0 ? 5 : 8))) void conv_fork_kernel(
     const TX* __restrict__ raw0, const TX* __restrict__ rawt, const TW* __restrict__ w,
     const TW* __restrict__ bias, TX* __restrict__ y0, TX* __restrict__ yt, TX* __restrict__ tails,
-    int L, int Cd, int block, int cold_noised) {
+    int L, int Cd, int block, int cold_noised, int kb_off) {
   const int cg = blockIdx.x * blockDim.x + threadIdx.x;  // channel group
   const int c0 = cg * VEC;
   if (c0 >= Cd) return;
   if (BLK > 0) block = BLK;
-  const int kblk = blockIdx.y;
+  const int kblk = blockIdx.y + kb_off;  // the launch covers blocks [kb_off, kb_off + gridDim.y)
   const int b = blockIdx.z;
   const int nb = L / block;
 
@@ -168,9 +168,9 @@ __global__ __launch_bounds__(256) void conv_generic_kernel(
 
 template <typename TX, typename TW>
 static int launch_fork(const void* raw0, const void* rawt, const void* w, const void* bias, void* y0,
-                       void* yt, void* tails, int B, int L, int Cd, int K, int block, int cold,
-                       hipStream_t st) {
-  const int nb = L / block;
+                       void* yt, void* tails, int B, int L, int Cd, int K, int block, int cold, int kb0,
+                       int nkb, hipStream_t st) {
+  const int nb = nkb;  // blocks of this launch, from kb0
   constexpr int V = 16 / sizeof(TX);  // 16-byte row segments per thread
   const bool vec_ok = (Cd % V == 0) && ((uintptr_t)raw0 % 16 == 0) && ((uintptr_t)rawt % 16 == 0) &&
                       ((uintptr_t)y0 % 16 == 0) && ((uintptr_t)yt % 16 == 0) &&
@@ -184,7 +184,7 @@ static int launch_fork(const void* raw0, const void* rawt, const void* w, const 
       dim3 grid((groups + 255) / 256, nb, B);
       conv_fork_kernel<TX, TW, 4, 4, 32><<<grid, 256, 0, st>>>(
           (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-          Cd, block, cold);
+          Cd, block, cold, kb0);
       done = true;
     }
   }
@@ -194,22 +194,22 @@ static int launch_fork(const void* raw0, const void* rawt, const void* w, const 
     dim3 grid((groups + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 4, V, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold);
+        Cd, block, cold, kb0);
   } else if (K == 4) {
     dim3 grid((Cd + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 4, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold);
+        Cd, block, cold, kb0);
   } else if (K == 2) {
     dim3 grid((Cd + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 2, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold);
+        Cd, block, cold, kb0);
   } else if (K == 3) {
     dim3 grid((Cd + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 3, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold);
+        Cd, block, cold, kb0);
   } else {
     return fail(DLLM_EUNSUPPORTED, "conv fork: kernel width %d not supported (2, 3 or 4)", K);
   }
@@ -222,25 +222,43 @@ static int launch_fork(const void* raw0, const void* rawt, const void* w, const 
 
 using namespace dllm;
 
-extern "C" int dllm_conv_fork_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,
-                                  void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
-                                  int block, int dtype_x, int dtype_w, int flags, void* stream) {
+// The fork conv over blocks [kb0, kb1) of every sequence.
+static int conv_fork(const void* raw0, const void* rawt, const void* weight, const void* bias, void* y0, void* yt,
+                     void* tails, int B, int L, int conv_dim, int width, int block, int dtype_x, int dtype_w,
+                     int flags, int kb0, int kb1, hipStream_t st) {
   if (!raw0 || !rawt || !weight || !y0 || !yt) return fail(DLLM_EINVAL, "conv fork: null pointer");
   if (B <= 0 || L <= 0 || conv_dim <= 0 || block <= 0)
     return fail(DLLM_EINVAL, "conv fork: bad sizes B=%d L=%d conv_dim=%d block=%d", B, L, conv_dim, block);
   if (L % block) return fail(DLLM_EINVAL, "L=%d is not a multiple of block=%d", L, block);
   if (L / block > 65535 || B > 65535) return fail(DLLM_EUNSUPPORTED, "conv fork: grid too large");
-  const int cold = flags & 1;
-  hipStream_t st = (hipStream_t)stream;
+  if (kb0 < 0 || kb1 > L / block || kb0 >= kb1)
+    return fail(DLLM_EINVAL, "conv fork: block range [%d, %d) of %d", kb0, kb1, L / block);
+  const int cold = flags & 1, n = kb1 - kb0;
   if (dtype_x == DT_BF16 && dtype_w == DT_BF16)
-    return launch_fork<bf16, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, st);
+    return launch_fork<bf16, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
   if (dtype_x == DT_F32 && dtype_w == DT_F32)
-    return launch_fork<float, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, st);
+    return launch_fork<float, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
   if (dtype_x == DT_BF16 && dtype_w == DT_F32)
-    return launch_fork<bf16, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, st);
+    return launch_fork<bf16, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
   if (dtype_x == DT_F32 && dtype_w == DT_BF16)
-    return launch_fork<float, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, st);
+    return launch_fork<float, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
   return fail(DLLM_EUNSUPPORTED, "conv fork: dtype pair (%d, %d) not supported", dtype_x, dtype_w);
+}
+
+extern "C" int dllm_conv_fork_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,
+                                  void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
+                                  int block, int dtype_x, int dtype_w, int flags, void* stream) {
+  const int nb = block > 0 && L > 0 && L % block == 0 ? L / block : 1;  // sizes are checked by conv_fork
+  return conv_fork(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, dtype_x, dtype_w, flags, 0,
+                   nb, (hipStream_t)stream);
+}
+
+extern "C" int dllm_conv_fork_range_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,
+                                        void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
+                                        int block, int dtype_x, int dtype_w, int flags, int block_begin,
+                                        int block_end, void* stream) {
+  return conv_fork(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, dtype_x, dtype_w, flags,
+                   block_begin, block_end, (hipStream_t)stream);
 }
 
 extern "C" int dllm_causal_conv1d_fwd(const void* x, const int64_t* x_strides, const void* prefix,

@@ -55,6 +55,11 @@ struct GdnArgs {
   int vec_v;   // v rows: 16-byte vector loads (aligned, Dv a multiple of the column window)
   int spin_limit;  // bounded waits give up (and report through dllm_status) after this many sleeps
   int wait_bias;   // 0; tests set a count the LDS wait never reaches, to exercise the give-up path
+  // pipelined fork over a range of blocks: rows and snapshots per sequence of the full out and
+  // states tensors (T and T / sub for a whole sequence), and the clean state the range starts
+  // from (the snapshot of the block before it, in the states layout; null: zeros)
+  int t_rows, snap_rows;
+  const float* fork_init;
 };
 
 // Linear workgroup id such that consecutive ids run on the same XCD (dispatch is round-robin over
@@ -1216,6 +1221,13 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   f32x16 S[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) S[t] = zero16();
+  if (a.fork_init) {  // a range after the first block: the snapshot before it (rows as stored below)
+    const float* ip = a.fork_init + ((long long)b * a.snap_rows * a.Hv + hv) * (128LL * 128) + u * 32 + 16 * h * 128 + l32;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) S[kt][v] = ip[(32 * kt + v) * 128];
+  }
   for (int c = -1; c < ntiles; ++c) {
     __syncthreads();  // tile c-1's state phase and tile c's preparation are done
     if (c >= 0) {
@@ -1312,7 +1324,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           mma32(accQS[s], fp, fv);
         }
         {
-          bf16* ob = (bf16*)a.s[s].out + ((long long)b * a.T + t0) * rs + (long long)hv * a.Dv + u * 32;
+          bf16* ob = (bf16*)a.s[s].out + ((long long)b * a.t_rows + t0) * rs + (long long)hv * a.Dv + u * 32;
           const unsigned lo2 = (unsigned)(4 * h * rs + l32);
           if (a.sub == 32) {
 #pragma unroll
@@ -1338,7 +1350,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           F fd;
           acc_to_frag(vd, fd);
           // accumulator row rho(v, h) of slice kt is state row 32 kt + 16 h + v
-          float* const sb = a.states ? a.states + (((long long)b * ntiles + c) * a.Hv + hv) * (128LL * 128) + u * 32 +
+          float* const sb = a.states ? a.states + (((long long)b * a.snap_rows + c) * a.Hv + hv) * (128LL * 128) + u * 32 +
                                            16 * h * 128 + l32
                                      : nullptr;
 #pragma unroll
@@ -1481,10 +1493,12 @@ extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const
   return dispatch_gdn(a, dtype, false, (hipStream_t)stream);
 }
 
-extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, int64_t qkv_stride_t,
-                                       const float* beta0, const float* betat, const float* g0, const float* gt,
-                                       void* out0, void* outt, float* states, int B, int L, int Hk, int Hv, int Dk,
-                                       int Dv, int block, int dtype, float scale, void* stream) {
+// The state fork over blocks [kb0, kb1) of every sequence (the whole sequence: [0, L / block)).
+// A range after the first block starts from states[:, kb0 - 1] and runs the pipelined kernel only.
+static int state_fork(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, int64_t qkv_stride_t,
+                      const float* beta0, const float* betat, const float* g0, const float* gt, void* out0,
+                      void* outt, float* states, int B, int L, int Hk, int Hv, int Dk, int Dv, int block, int dtype,
+                      float scale, int kb0, int kb1, void* stream) {
   if (!qkv0 || !qkvt || !beta0 || !betat || !g0 || !gt || !out0 || !outt) return fail(DLLM_EINVAL, "gdn fork: null pointer");
   if (B <= 0 || L <= 0 || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0 || block <= 0)
     return fail(DLLM_EINVAL, "gdn fork: bad sizes");
@@ -1494,12 +1508,17 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
     return fail(DLLM_EUNSUPPORTED, "gdn fork: fused fork unsupported for Dk=%d block=%d dtype=%d", Dk, block, dtype);
   if (!fits_i32((long long)L * qkv_stride_t) || !fits_i32((long long)L * Hv))
     return fail(DLLM_EUNSUPPORTED, "gdn fork: per-sequence extent exceeds 32-bit element offsets");
+  const int nb = L / block;
+  if (kb0 < 0 || kb1 > nb || kb0 >= kb1) return fail(DLLM_EINVAL, "gdn fork: block range [%d, %d) of %d", kb0, kb1, nb);
+  const bool whole = kb0 == 0 && kb1 == nb;
+  if (kb0 > 0 && !states) return fail(DLLM_EINVAL, "gdn fork: a range after block 0 starts from states (null)");
   GdnArgs a = {};
   const int esz = dtype == DT_BF16 ? 2 : 4;
-  const char* base[2] = {(const char*)qkv0, (const char*)qkvt};
-  const float* bet[2] = {beta0, betat};
-  const float* gg[2] = {g0, gt};
-  void* outs[2] = {out0, outt};
+  const long long t_off = (long long)kb0 * block;  // first row of the range
+  const char* base[2] = {(const char*)qkv0 + t_off * qkv_stride_t * esz, (const char*)qkvt + t_off * qkv_stride_t * esz};
+  const float* bet[2] = {beta0 + t_off * Hv, betat + t_off * Hv};
+  const float* gg[2] = {g0 + t_off * Hv, gt + t_off * Hv};
+  void* outs[2] = {(char*)out0 + t_off * Hv * Dv * esz, (char*)outt + t_off * Hv * Dv * esz};
   for (int i = 0; i < 2; ++i) {
     GdnStream& s = a.s[i];
     s.q = base[i];
@@ -1517,8 +1536,12 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
   a.b_st = a.g_st = Hv;
   a.b_sh = a.g_sh = 1;
   a.init = nullptr;
-  a.states = states;
-  a.B = B; a.T = L; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv;
+  const long long snap_elems = (long long)Hv * Dk * Dv;
+  a.states = states ? states + kb0 * snap_elems : nullptr;
+  a.fork_init = kb0 > 0 ? states + (kb0 - 1) * snap_elems : nullptr;
+  a.t_rows = L;
+  a.snap_rows = nb;
+  a.B = B; a.T = (kb1 - kb0) * block; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv;
   a.sub = block;
   a.snap_every = 1;
   a.scale = scale;
@@ -1533,7 +1556,26 @@ extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64
   a.vec_v = aligned16(qkv0) && aligned16(qkvt) && st_ok && (Dv % window_for(dtype) == 0);
   // full 128 x 128 heads with 16-byte rows: the pipelined kernel
   if (dtype == DT_BF16 && Dk == 128 && Dv == 128 && a.vec_qk && a.vec_v) return launch_fork_pipe(a, (hipStream_t)stream);
+  if (!whole) return fail(DLLM_EUNSUPPORTED, "gdn fork: block ranges need the pipelined kernel (bf16, Dk = Dv = 128)");
   return dispatch_gdn(a, dtype, true, (hipStream_t)stream);
+}
+
+extern "C" int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, int64_t qkv_stride_t,
+                                       const float* beta0, const float* betat, const float* g0, const float* gt,
+                                       void* out0, void* outt, float* states, int B, int L, int Hk, int Hv, int Dk,
+                                       int Dv, int block, int dtype, float scale, void* stream) {
+  const int nb = block > 0 && L > 0 && L % block == 0 ? L / block : 1;  // sizes are checked by state_fork
+  return state_fork(qkv0, qkvt, qkv_stride_b, qkv_stride_t, beta0, betat, g0, gt, out0, outt, states, B, L, Hk, Hv,
+                    Dk, Dv, block, dtype, scale, 0, nb, stream);
+}
+
+extern "C" int dllm_gdn_state_fork_range_fwd(const void* qkv0, const void* qkvt, int64_t qkv_stride_b,
+                                             int64_t qkv_stride_t, const float* beta0, const float* betat,
+                                             const float* g0, const float* gt, void* out0, void* outt, float* states,
+                                             int B, int L, int Hk, int Hv, int Dk, int Dv, int block, int dtype,
+                                             float scale, int block_begin, int block_end, void* stream) {
+  return state_fork(qkv0, qkvt, qkv_stride_b, qkv_stride_t, beta0, betat, g0, gt, out0, outt, states, B, L, Hk, Hv,
+                    Dk, Dv, block, dtype, scale, block_begin, block_end, stream);
 }
 
 extern "C" int dllm_set_spin_limit(int limit) {

@@ -41,9 +41,16 @@ _SIGNATURES = {
     "dllm_gdn_state_fork_fwd": (_c_int, [
         _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p, _c_fp, _c_fp, _c_void_p, _c_void_p,
         _c_fp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_void_p]),
+    "dllm_gdn_state_fork_range_fwd": (_c_int, [
+        _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p, _c_fp, _c_fp, _c_void_p, _c_void_p,
+        _c_fp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int,
+        _c_void_p]),
     "dllm_conv_fork_fwd": (_c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+    "dllm_conv_fork_range_fwd": (_c_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "dllm_causal_conv1d_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p]),

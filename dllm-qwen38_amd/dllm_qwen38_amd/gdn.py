@@ -393,3 +393,51 @@ class StateForkPlan:
         self.run_conv(stream)
         self.run_core(stream)
         _IMPL["last"], _IMPL["reason"] = "hip", ""
+
+    def overlap_supported(self):
+        """Whether run_overlapped can split this plan's layer (the pipelined fork path, states kept)."""
+        B, L, Cd, Hk, Hv, Dk, Dv, block = self.dims
+        return (self.states is not None and L // block >= 2
+                and self._lib.dllm_gdn_state_fork_path(Dk, Dv, block, self.code) == 2)
+
+    def run_overlapped(self, pieces=4, bounds=None):
+        """The layer cut into `pieces` ranges of blocks (or at the given block boundaries, e.g.
+        [0, 16, 64, 128]): the conv of each range runs on a side stream while the fork of the range
+        before it runs on the caller's stream, which waits for each range's conv by an event; each
+        fork range starts from the snapshot the one before it wrote. The results equal run()'s bit
+        for bit. Enqueued on the current stream."""
+        if not self.overlap_supported():
+            raise ValueError("run_overlapped needs the pipelined fork path with states")
+        B, L, Cd, Hk, Hv, Dk, Dv, block = self.dims
+        nb = L // block
+        if bounds is not None:
+            cuts = [int(c) for c in bounds]
+            if cuts[0] != 0 or cuts[-1] != nb or any(b <= a for a, b in zip(cuts, cuts[1:])):
+                raise ValueError(f"bounds must rise from 0 to {nb}")
+        else:
+            pieces = max(1, min(int(pieces), nb))
+            cuts = [nb * i // pieces for i in range(pieces + 1)]
+        pieces = len(cuts) - 1
+        if not hasattr(self, "_side"):
+            self._side = torch.cuda.Stream(device=self.device)
+            self._events = []
+        while len(self._events) < pieces:
+            self._events.append(torch.cuda.Event())
+        main = torch.cuda.current_stream(self.device)
+        bounds = list(zip(cuts, cuts[1:]))
+        wc = _lib.dtype_code(self.w.dtype)
+        self._side.wait_stream(main)
+        for i, (k0, k1) in enumerate(bounds):
+            _lib.check(self._lib.dllm_conv_fork_range_fwd(
+                self.raw0.data_ptr(), self.rawt.data_ptr(), self.w.data_ptr(), None, self.y0.data_ptr(),
+                self.yt.data_ptr(), _lib.ptr(self.tails), B, L, Cd, self.K, block, self.code, wc, 0, k0, k1,
+                self._side.cuda_stream), "dllm_conv_fork_range_fwd")
+            self._events[i].record(self._side)
+        for i, (k0, k1) in enumerate(bounds):
+            main.wait_event(self._events[i])
+            _lib.check(self._lib.dllm_gdn_state_fork_range_fwd(
+                self.y0.data_ptr(), self.yt.data_ptr(), L * Cd, Cd, self.beta0.data_ptr(), self.betat.data_ptr(),
+                self.g0.data_ptr(), self.gt.data_ptr(), self.o0.data_ptr(), self.ot.data_ptr(),
+                _lib.ptr(self.states), B, L, Hk, Hv, Dk, Dv, block, self.code, Dk ** -0.5, k0, k1,
+                main.cuda_stream), "dllm_gdn_state_fork_range_fwd")
+        _IMPL["last"], _IMPL["reason"] = "hip", ""

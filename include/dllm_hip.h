@@ -83,6 +83,22 @@ int dllm_gdn_state_fork_fwd(const void* qkv0, const void* qkvt, int64_t qkv_stri
                             int Dv, int block, int dtype, float scale, void* stream);
 
 /*
+ * The same op over blocks [block_begin, block_end) of every sequence, for callers that overlap the
+ * conv of later blocks with the fork of earlier ones (the reference has no such split: it is the
+ * blockdiff.py:153-177 arm above, cut along the sequence). All pointers and sizes are those of the
+ * whole op; outputs and states are written for the range only. A range after block 0 starts from
+ * the clean state after block block_begin - 1, read from states (which must not be NULL and must
+ * hold that snapshot, as the range before it writes). Ranges run the pipelined fork kernel only
+ * (dllm_gdn_state_fork_path() == 2); other shapes return -2 (unsupported) unless the range is the
+ * whole sequence. Running consecutive ranges in order gives the whole op's results bit for bit.
+ */
+int dllm_gdn_state_fork_range_fwd(const void* qkv0, const void* qkvt, int64_t qkv_stride_b,
+                                  int64_t qkv_stride_t, const float* beta0, const float* betat,
+                                  const float* g0, const float* gt, void* out0, void* outt, float* states,
+                                  int B, int L, int Hk, int Hv, int Dk, int Dv, int block, int dtype,
+                                  float scale, int block_begin, int block_end, void* stream);
+
+/*
  * Bounded waits inside kernels (the pipelined fork's LDS row-buffer hand-off between its waves)
  * give up after a limit and set a bit in a per-device status word instead of hanging:
  * 1 = LDS row-buffer wait; a launch that set a bit produced invalid outputs.
@@ -111,6 +127,16 @@ int dllm_set_wait_test_mode(int on);
 int dllm_conv_fork_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,
                        void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
                        int block, int dtype_x, int dtype_w, int flags, void* stream);
+
+/*
+ * dllm_conv_fork_fwd over blocks [block_begin, block_end) of every sequence (rows, tails and the
+ * prefix carry-in of those blocks; the carry-in reads the rows before block_begin). The split that
+ * dllm_gdn_state_fork_range_fwd takes, for the same overlap; no counterpart in the reference.
+ */
+int dllm_conv_fork_range_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,
+                             void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
+                             int block, int dtype_x, int dtype_w, int flags, int block_begin,
+                             int block_end, void* stream);
 
 /*
  * Generic causal depthwise conv (+ optional SiLU) with an optional prefix.

@@ -1,0 +1,79 @@
+"""The state-fork layer cut into block ranges (StateForkPlan.run_overlapped): the conv of each range
+runs on a side stream beside the fork of the range before it, and each fork range starts from the
+fp32 snapshot the range before it wrote. Every output must equal the one-launch schedule (run())
+bit for bit: the snapshot is the exact register state, and a block's arithmetic does not depend on
+where a launch starts. Slow decay (g shift -4) keeps the carried state visible in the outputs.
+
+Also the range entry points' argument checks (a range after block 0 needs the states tensor;
+ranges need the pipelined kernel; the range must lie inside the sequence)."""
+
+import pytest
+import torch
+
+from dllm_qwen38_amd import _lib, gdn, inputs
+
+pytestmark = pytest.mark.gpu
+
+OUTS = ("y0", "yt", "tails", "o0", "ot", "states")
+
+
+def _plan(dev, s, B, L, g_shift):
+    x = {k: v.to(dev) for k, v in inputs.gdn_layer_inputs(s, B=B, L=L, g_shift=g_shift).items()}
+    return gdn.StateForkPlan(x["raw0"], x["rawt"], x["conv_w"], x["beta0"], x["betat"], x["g0"], x["gt"],
+                             num_k_heads=s.Hk, num_v_heads=s.Hv, head_k_dim=s.D, head_v_dim=s.D, block=s.block)
+
+
+@pytest.mark.parametrize("shape,B,L", [("GDN_27B_BF16", 1, 512), ("GDN_08B_BF16", 2, 1024)])
+def test_overlapped_schedule_is_bit_identical(dev, shape, B, L):
+    s = getattr(inputs, shape)
+    p = _plan(dev, s, B, L, g_shift=-4.0)
+    assert p.overlap_supported()
+    p.run()
+    torch.cuda.synchronize()
+    ref = {k: getattr(p, k).clone() for k in OUTS}
+    nb = L // s.block
+    for kw in ({"pieces": 2}, {"pieces": 3}, {"pieces": 5}, {"bounds": [0, 1, nb // 2, nb]},
+               {"bounds": [0, nb - 1, nb]}):
+        for k in OUTS:
+            getattr(p, k).fill_(float("nan"))
+        print(f"{shape} B={B} L={L} run_overlapped({kw})", flush=True)
+        p.run_overlapped(**kw)
+        torch.cuda.synchronize()
+        for k in OUTS:
+            assert torch.equal(getattr(p, k), ref[k]), (kw, k)
+    assert gdn.kernel_status(reset=True) == 0
+
+
+def test_range_entry_argument_checks(dev):
+    s = inputs.GDN_27B_BF16
+    B, L = 1, 256
+    p = _plan(dev, s, B, L, g_shift=None)
+    lib = _lib.lib()
+    Cd = p.dims[2]
+
+    def fork(states, k0, k1, Dk=s.D):
+        return lib.dllm_gdn_state_fork_range_fwd(
+            p.y0.data_ptr(), p.yt.data_ptr(), L * Cd, Cd, p.beta0.data_ptr(), p.betat.data_ptr(), p.g0.data_ptr(),
+            p.gt.data_ptr(), p.o0.data_ptr(), p.ot.data_ptr(), states, B, L, s.Hk, s.Hv, Dk, s.D, s.block,
+            p.code, s.D ** -0.5, k0, k1, _lib.stream_handle(dev))
+
+    def conv(k0, k1):
+        return lib.dllm_conv_fork_range_fwd(
+            p.raw0.data_ptr(), p.rawt.data_ptr(), p.w.data_ptr(), None, p.y0.data_ptr(), p.yt.data_ptr(),
+            p.tails.data_ptr(), B, L, Cd, p.K, s.block, p.code, _lib.dtype_code(p.w.dtype), 0, k0, k1,
+            _lib.stream_handle(dev))
+
+    nb = L // s.block
+    assert fork(None, 2, nb) == -1  # a range after block 0 starts from states
+    assert fork(p.states.data_ptr(), 0, nb + 1) == -1
+    assert fork(p.states.data_ptr(), 3, 3) == -1
+    assert conv(-1, 2) == -1
+    assert conv(4, nb + 1) == -1
+    assert conv(5, 5) == -1
+    msg = _lib.last_error()
+    assert "block range" in msg, msg
+    torch.cuda.synchronize()
+    # nothing was launched by the rejected calls; a valid pair of ranges still runs
+    assert conv(0, nb) == 0 and fork(p.states.data_ptr(), 0, nb) == 0
+    torch.cuda.synchronize()
+    assert gdn.kernel_status(reset=True) == 0

@@ -31,6 +31,20 @@ HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 
+def _calibration_copy(a, dev):
+    """With --calibration-copy-gib G: one device-to-device copy of G GiB after the timed steps, the
+    known-size kernel that PMC traffic counts are scaled by."""
+    import torch
+
+    if a.calibration_copy_gib > 0:
+        n = int(a.calibration_copy_gib * (1 << 28))
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
+
+
 def _traffic_from_profiles(name):
     """HBM bytes per launch of the dominant kernel from a committed PMC summary, if present."""
     p = os.path.join(ROOT, "profiles", name)
@@ -231,13 +245,7 @@ def bench_gdn_layer(a):
         "wall_s_timed": wall,
         "cpu_baseline": None,
     }
-    if a.calibration_copy_gib > 0:
-        n = int(a.calibration_copy_gib * (1 << 28))
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize(dev)
-        del src, dst
+    _calibration_copy(a, dev)
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(s, min(a.cpu_sample_L, s.L), a.cpu_budget_s)
         res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
@@ -288,9 +296,11 @@ def bench_attention(a):
         "config": {"workload": "complementary-mask attention, B=2 L=4096 block 32 Hq=24 Hkv=4 d=256 over "
                                "cat([x_t, x_0]), bf16", "global_batch": B, "seq_len": L, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tf / BF16_MFMA_PEAK_TFLOPS, "traffic": None},
+                     "frac": tf / BF16_MFMA_PEAK_TFLOPS,
+                     "traffic": _traffic_from_profiles("attention_config4_traffic.json")},
         "algorithmic_gflop": fl / 1e9, "wall_s_timed": wall, "cpu_baseline": None,
     }
+    _calibration_copy(a, dev)
     if not a.no_cpu_baseline:
         sys.path.insert(0, ROOT)
         from oracle import attn_ref

@@ -27,6 +27,8 @@
 // whole sequence and is fed back as the B operand directly from the accumulator layout.
 #include <type_traits>
 
+#include <atomic>
+
 #include "common.h"
 
 namespace dllm {
@@ -839,6 +841,12 @@ __device__ __forceinline__ void report_status(unsigned bit) {
   __hip_atomic_fetch_or(&dllm_status_word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// SPLIT: one workgroup per (sequence, value head, half of the value columns): state waves 0 and 1
+// own columns [64 half + 32 u, +32) and state waves 2 and 3 only keep the barrier and counter
+// sequence. The G and P waves prepare the whole tile in both workgroups of a head. For batches
+// whose (sequence, head) count fills half the chip or less (measured: 302-306 vs 312-317 us at
+// B = 8, Hv = 16, bit-identical).
+template <bool SPLIT>
 __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   using SM = PipeSmem;
   using F = Frag<true>;
@@ -855,9 +863,12 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   const int gs = u >> 1;             // prep waves: stream prepared (0 clean, 1 noised)
   const bool isG = prep && (u & 1) == 0;
 
-  const int lin = xcd_linear_id(blockIdx.x, gridDim.x);
-  const int hv = lin % a.Hv;
-  const int b = lin / a.Hv;
+  const int lin = xcd_linear_id(blockIdx.x, gridDim.x);  // the halves of a head: one XCD
+  const int half = SPLIT ? lin & 1 : 0;
+  const int hv = (SPLIT ? lin >> 1 : lin) % a.Hv;
+  const int b = (SPLIT ? lin >> 1 : lin) / a.Hv;
+  const bool idle = SPLIT && !prep && u >= 2;
+  const int cu = SPLIT ? half * 64 + (u & 1) * 32 : u * 32;  // first value column of a state wave
   const int hk = hv / (a.Hv / a.Hk);
   const int ntiles = a.T / a.sub;
 
@@ -1222,7 +1233,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
 #pragma unroll
   for (int t = 0; t < KT; ++t) S[t] = zero16();
   if (a.fork_init) {  // a range after the first block: the snapshot before it (rows as stored below)
-    const float* ip = a.fork_init + ((long long)b * a.snap_rows * a.Hv + hv) * (128LL * 128) + u * 32 + 16 * h * 128 + l32;
+    const float* ip = a.fork_init + ((long long)b * a.snap_rows * a.Hv + hv) * (128LL * 128) + cu + 16 * h * 128 + l32;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
@@ -1230,6 +1241,10 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   }
   for (int c = -1; c < ntiles; ++c) {
     __syncthreads();  // tile c-1's state phase and tile c's preparation are done
+    if (idle) {  // the other half's columns: count as done reading the tile's rows
+      if (c >= 0 && lane == 0) __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      continue;
+    }
     if (c >= 0) {
       // ---------------------------------------------------------- state phase, tile c
       const int pc = c & 1;
@@ -1291,7 +1306,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
         const bf16x8* t1 = T1f(s, pc) + 2 * lane;
         ft1.lo = t1[0];
         ft1.hi = t1[1];
-        lds_frag_tr(VB(s, pc) + u * 32, QROW, lane, fv);
+        lds_frag_tr(VB(s, pc) + cu, QROW, lane, fv);
         acc_to_frag(accKS[s], fks);
         mma32(accV[s], ft, fv);    // U = T2 V
         mma32(accV[s], ft1, fks);  // - T1 K S
@@ -1324,7 +1339,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           mma32(accQS[s], fp, fv);
         }
         {
-          bf16* ob = (bf16*)a.s[s].out + ((long long)b * a.t_rows + t0) * rs + (long long)hv * a.Dv + u * 32;
+          bf16* ob = (bf16*)a.s[s].out + ((long long)b * a.t_rows + t0) * rs + (long long)hv * a.Dv + cu;
           const unsigned lo2 = (unsigned)(4 * h * rs + l32);
           if (a.sub == 32) {
 #pragma unroll
@@ -1350,7 +1365,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           F fd;
           acc_to_frag(vd, fd);
           // accumulator row rho(v, h) of slice kt is state row 32 kt + 16 h + v
-          float* const sb = a.states ? a.states + (((long long)b * a.snap_rows + c) * a.Hv + hv) * (128LL * 128) + u * 32 +
+          float* const sb = a.states ? a.states + (((long long)b * a.snap_rows + c) * a.Hv + hv) * (128LL * 128) + cu +
                                            16 * h * 128 + l32
                                      : nullptr;
 #pragma unroll
@@ -1382,10 +1397,31 @@ static int launch_gdn(const GdnArgs& a, hipStream_t st) {
   return DLLM_OK;
 }
 
+// Compute units of the current device (cached per device; 0 if the query fails).
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// 0: split a head's columns over two workgroups when the split grid fits the chip; 1: never;
+// 2: always (dllm_set_fork_split, for tests)
+static std::atomic<int> g_fork_split{0};
+
 static int launch_fork_pipe(const GdnArgs& a, hipStream_t st) {
-  const long long nblk = (long long)a.B * a.Hv;
+  const long long heads = (long long)a.B * a.Hv;
+  const int mode = g_fork_split.load(std::memory_order_relaxed);
+  const bool split = mode == 2 || (mode == 0 && 2 * heads <= device_cus());
+  const long long nblk = split ? 2 * heads : heads;
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "gdn: grid too large");
-  gdn_fork_pipe_kernel<<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  if (split) gdn_fork_pipe_kernel<true><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  else gdn_fork_pipe_kernel<false><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "gdn fork launch: %s", hipGetErrorString(e));
   return DLLM_OK;
@@ -1576,6 +1612,11 @@ extern "C" int dllm_gdn_state_fork_range_fwd(const void* qkv0, const void* qkvt,
                                              float scale, int block_begin, int block_end, void* stream) {
   return state_fork(qkv0, qkvt, qkv_stride_b, qkv_stride_t, beta0, betat, g0, gt, out0, outt, states, B, L, Hk, Hv,
                     Dk, Dv, block, dtype, scale, block_begin, block_end, stream);
+}
+
+extern "C" int dllm_set_fork_split(int mode) {
+  if (mode < 0 || mode > 2) return fail(DLLM_EINVAL, "fork split mode %d (0 auto, 1 never, 2 always)", mode);
+  return g_fork_split.exchange(mode);
 }
 
 extern "C" int dllm_set_spin_limit(int limit) {

@@ -36,6 +36,7 @@ _SIGNATURES = {
     "dllm_gdn_fused_fork_supported": (_c_int, [_c_int, _c_int, _c_int]),
     "dllm_gdn_state_fork_path": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "dllm_set_spin_limit": (_c_int, [_c_int]),
+    "dllm_set_fork_split": (_c_int, [_c_int]),
     "dllm_status": (_c_int, [_c_int]),
     "dllm_set_wait_test_mode": (_c_int, [_c_int]),
     "dllm_gdn_state_fork_fwd": (_c_int, [

@@ -109,6 +109,13 @@ int dllm_gdn_state_fork_range_fwd(const void* qkv0, const void* qkvt, int64_t qk
  */
 int dllm_status(int reset);
 int dllm_set_spin_limit(int limit);
+/*
+ * The pipelined fork splits each head's value columns over two workgroups when twice the
+ * (sequence, value head) count fits the device's compute units (mode 0, the default); mode 1
+ * never splits, mode 2 always does. Results are identical either way. Process-wide; returns the
+ * previous mode. For tests and measurement; no counterpart in the reference.
+ */
+int dllm_set_fork_split(int mode);
 /* Test only: with on != 0, the LDS row-buffer wait waits for a count that is never reached, so
  * every such wait gives up after the spin limit (the kernel still ends, outputs invalid). Returns
  * the previous mode. */

@@ -77,3 +77,30 @@ def test_range_entry_argument_checks(dev):
     assert conv(0, nb) == 0 and fork(p.states.data_ptr(), 0, nb) == 0
     torch.cuda.synchronize()
     assert gdn.kernel_status(reset=True) == 0
+
+
+@pytest.mark.parametrize("shape,B,L", [("GDN_27B_BF16", 1, 512), ("GDN_08B_BF16", 2, 1024)])
+def test_column_split_of_the_fork_is_bit_identical(dev, shape, B, L):
+    """The pipelined fork with each head's value columns over two workgroups (the default when
+    the split grid fits the chip) against one workgroup per head: identical outputs and states
+    (every column is computed by the same arithmetic in either layout)."""
+    s = getattr(inputs, shape)
+    p = _plan(dev, s, B, L, g_shift=-4.0)
+    lib = _lib.lib()
+    got = {}
+    prev = lib.dllm_set_fork_split(1)
+    try:
+        for mode in (1, 2):
+            lib.dllm_set_fork_split(mode)
+            for k in OUTS[3:]:
+                getattr(p, k).fill_(float("nan"))
+            print(f"{shape} B={B} L={L} split mode {mode}", flush=True)
+            p.run()
+            torch.cuda.synchronize()
+            got[mode] = {k: getattr(p, k).clone() for k in OUTS[3:]}
+    finally:
+        lib.dllm_set_fork_split(prev)
+    for k in OUTS[3:]:
+        assert torch.equal(got[1][k], got[2][k]), k
+    assert lib.dllm_set_fork_split(3) == -1
+    assert gdn.kernel_status(reset=True) == 0

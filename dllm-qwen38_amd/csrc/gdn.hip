@@ -1464,8 +1464,8 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Sleeps after which a bounded wait gives up and sets a dllm_status bit (process-wide; tests lower
 // it to force that path).
-static int g_spin_limit = 1 << 20;
-static int g_wait_bias = 0;  // dllm_set_wait_test_mode
+static std::atomic<int> g_spin_limit{1 << 20};
+static std::atomic<int> g_wait_bias{0};  // dllm_set_wait_test_mode
 
 static bool fits_i32(long long x) { return x >= -2147483647LL && x <= 2147483647LL; }
 
@@ -1518,8 +1518,8 @@ extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const
   a.snap_every = chunk / a.sub;
   a.scale = scale;
   a.l2norm = use_qk_l2norm;
-  a.spin_limit = g_spin_limit;
-  a.wait_bias = g_wait_bias;
+  a.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
+  a.wait_bias = g_wait_bias.load(std::memory_order_relaxed);
   const int esz = dtype == DT_BF16 ? 2 : 4;
   const int vel = 16 / esz;
   auto st_ok = [&](const int64_t* st3) { return (st3[0] % vel == 0) && (st3[1] % vel == 0) && (st3[2] % vel == 0); };
@@ -1582,8 +1582,8 @@ static int state_fork(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, 
   a.snap_every = 1;
   a.scale = scale;
   a.l2norm = 1;
-  a.spin_limit = g_spin_limit;
-  a.wait_bias = g_wait_bias;
+  a.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
+  a.wait_bias = g_wait_bias.load(std::memory_order_relaxed);
   const int vel = 16 / esz;
   const bool st_ok = (qkv_stride_b % vel == 0) && (qkv_stride_t % vel == 0) && (Dk % vel == 0) && (Dv % vel == 0) &&
                      ((long long)Hk * Dk % vel == 0);
@@ -1621,9 +1621,7 @@ extern "C" int dllm_set_fork_split(int mode) {
 
 extern "C" int dllm_set_spin_limit(int limit) {
   if (limit < 0) return fail(DLLM_EINVAL, "spin limit %d < 0", limit);
-  const int prev = g_spin_limit;
-  g_spin_limit = limit;
-  return prev;
+  return g_spin_limit.exchange(limit);
 }
 
 extern "C" int dllm_status(int reset) {
@@ -1641,7 +1639,5 @@ extern "C" int dllm_status(int reset) {
 }
 
 extern "C" int dllm_set_wait_test_mode(int on) {
-  const int prev = g_wait_bias != 0;
-  g_wait_bias = on ? (1 << 30) : 0;
-  return prev;
+  return g_wait_bias.exchange(on ? (1 << 30) : 0) != 0;
 }

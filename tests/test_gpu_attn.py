@@ -42,6 +42,9 @@ def _check(got, ref, dtype, name, vmax=None):
     (1, 40, 4, 2, 64, 8),      # ragged length (L % 32 != 0)
     (2, 32, 4, 2, 16, 8),      # the tiny model's head size, padded to 32
     (1, 96, 2, 1, 32, 16),
+    (1, 200, 6, 1, 256, 8),    # d = 256, six query heads on one K/V head, ragged L, element masks
+    (3, 160, 4, 2, 256, 16),   # d = 256, query groups crossing blocks, B = 3
+    (1, 72, 2, 1, 128, 24),    # a block that is not a divisor of the 32-key tile
 ])
 def test_bd_attention_matches_oracle(dev, dtype, B, L, Hq, Hkv, d, block):
     q, k, v = _inputs(B, L, Hq, Hkv, d, dtype, seed=L + d + block)
@@ -63,8 +66,9 @@ def test_custom_scales(dev, scale):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_mask_leak_fault_matches_oracle_and_differs(dev, dtype):
-    q, k, v = _inputs(1, 64, 4, 2, 64, dtype, seed=5)
+@pytest.mark.parametrize("d", [64, 256])
+def test_mask_leak_fault_matches_oracle_and_differs(dev, dtype, d):
+    q, k, v = _inputs(1, 64, 4, 2, d, dtype, seed=5)
     good = attention.bd_attention(q.to(dev), k.to(dev), v.to(dev), block=16)
     bad = attention.bd_attention(q.to(dev), k.to(dev), v.to(dev), block=16, leak_xt_prefix=True)
     torch.cuda.synchronize()

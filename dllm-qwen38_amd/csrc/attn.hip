@@ -410,18 +410,18 @@ __device__ __forceinline__ void wait_vmcnt() {
 // ---------------------------------------------------------------------------------------------
 // bf16, d == D in {64, 128, 256}: eight waves, a pair per 32-query tile, split by role.
 // Waves 0..3 (S waves) hold Q^T of query tile u = wave and form S^T = K Q^T (lane = query), the mask
-// and the online softmax for key tile n; they hand P (the B-operand fragment of P^T, lane-major) and
-// the rescale factor of each query to their partner through an LDS ring of two slots. Waves 4..7
-// (O waves) hold O^T of the same query tile over the whole d and, one key tile behind, apply the
-// rescale and accumulate O^T += V^T P^T. No product is formed twice, an S wave holds no O and an O
-// wave no Q, and each SIMD runs one wave of each kind. (A split of the pair by halves of d instead
-// forms S in both waves: measured 1.25x the time at d = 256.) The hand-off needs no extra
-// synchronisation: slot n % 2 is written in the phase of tile n and read in the phase of tile
-// n + 1, across the one barrier per tile.
+// and the online softmax; they hand P (the B-operand fragment of P^T, lane-major) and the rescale
+// factor of each query to their partner through an LDS ring of two slots. Waves 4..7 (O waves)
+// hold O^T of the same query tile over the whole d and, one key tile behind, apply the rescale and
+// accumulate O^T += V^T P^T. No product is formed twice, an S wave holds no O and an O wave no Q,
+// and each SIMD runs one wave of each kind. (A split of the pair by halves of d instead forms S in
+// both waves: measured 1.25x the time at d = 256.) The hand-off needs no extra synchronisation:
+// slot n % 2 is written in the phase of tile n and read in the phase of tile n + 1, across the one
+// barrier per tile. The S waves are pipelined one tile ahead (the schedule is stated in the kernel).
 // K and V tiles travel global -> LDS by direct loads, no registers: each wave instruction moves
 // 1 KB = 64 lanes x 16 bytes; rows are dense with their 16-byte chunks XOR-swizzled (swz_key) so
-// that the K fragment reads and the V^T transpose reads are free of bank conflicts. A ring of four
-// stages is filled two tiles ahead (V of tile n - 1 stays in the ring while it is read).
+// that the K fragment reads and the V^T transpose reads are free of bank conflicts. K and V have
+// rings of their own, since a tile's K is read two phases before its V.
 // ---------------------------------------------------------------------------------------------
 // Max / sum of lane l's value and lane l ^ 32's (the two rows of an MFMA accumulator column),
 // exchanged by the gfx950 lane swap between the wave halves instead of through LDS. The sum's

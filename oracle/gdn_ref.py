@@ -142,8 +142,8 @@ def recurrent_gated_delta_rule_f64(q, k, v, g, beta, *, chunk_size=None, initial
         k = k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
     q = q * Dk ** -0.5
     S = (np.zeros((B, H, Dk, Dv)) if initial_state is None
-         else np.array(initial_state.detach().to(torch.float64) if torch.is_tensor(initial_state)
-                       else initial_state, dtype=np.float64).copy())
+         else (initial_state.detach().to(torch.float64).cpu().numpy() if torch.is_tensor(initial_state)
+               else np.asarray(initial_state, dtype=np.float64)).copy())
     o = np.zeros((B, T, H, Dv))
     snaps = []
     for t in range(T):

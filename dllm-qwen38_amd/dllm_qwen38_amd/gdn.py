@@ -14,6 +14,8 @@ q/k are never expanded.
 
 from __future__ import annotations
 
+import threading
+
 import torch
 
 from . import _lib, norms
@@ -203,7 +205,8 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
                    beta0: torch.Tensor, betat: torch.Tensor, g0: torch.Tensor, gt: torch.Tensor, *,
                    num_k_heads: int, num_v_heads: int, head_k_dim: int, head_v_dim: int, block: int,
                    conv_bias: torch.Tensor | None = None, need_states: bool = True,
-                   need_tails: bool = True, fault: str | None = None, out: dict | None = None):
+                   need_tails: bool = True, fault: str | None = None, out: dict | None = None,
+                   pieces: int | None = None):
     """The state-fork GDN layer core on pre-conv projections of both streams
     (reference blockdiff.py:153-177 with gdn.py:217-231, projections excluded).
 
@@ -212,7 +215,14 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     or None, tails [B*nb, conv_dim, K-1] or None).
 
     fault: None | "no-conv-prefix" (noised blocks' conv starts cold). `out` may pass preallocated
-    buffers (keys o0, ot, states, tails, y0, yt) to keep the call allocation-free."""
+    buffers (keys o0, ot, states, tails, y0, yt) to keep the call allocation-free.
+
+    pieces: the schedule. 1 runs the conv, then the fork, as two launches. k > 1 cuts the layer
+    into k ranges of blocks: the conv of each range runs on a side stream beside the fork of the
+    range before it (each fork range starts from the snapshot the one before wrote), which needs
+    the pipelined fork kernel and the states. None (default) takes 4 ranges where that applies and
+    the fork's grid leaves compute units free for the conv, else 1. Every schedule returns the same
+    results bit for bit."""
     dev = _lib.require_device(raw0, rawt, conv_weight, beta0, betat, g0, gt, conv_bias)
     if raw0.shape != rawt.shape or raw0.dim() != 3:
         raise ValueError("raw0 and rawt must both be [B, L, conv_dim]")
@@ -255,6 +265,22 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     wcode = _lib.dtype_code(w.dtype)
     cflags = 1 if fault == "no-conv-prefix" else 0
     bias = None if conv_bias is None else conv_bias.contiguous()
+    ranges_ok = states is not None and nb >= 2 and Lb.dllm_gdn_state_fork_path(Dk, Dv, block, code) == 2
+    if pieces is None:
+        pieces = default_pieces(_device_cus(dev), B, Hv, nb) if ranges_ok else 1
+    pieces = int(pieces)
+    if pieces < 1:
+        raise ValueError(f"pieces={pieces} must be at least 1")
+    if pieces > 1:
+        if not ranges_ok:
+            raise ValueError("pieces > 1 needs the pipelined fork kernel (bf16, Dk = Dv = 128), the states "
+                             "and at least two blocks")
+        pieces = min(pieces, nb)
+        cuts = [nb * i // pieces for i in range(pieces + 1)]
+        _launch_ranges(Lb, dev, cuts, (r0, rt, w, bias, y0, yt, tails, cflags),
+                       (y0, yt, b0, bt_, gg0, ggt, o0, ot, states), (B, L, Cd, K, Hk, Hv, Dk, Dv, block, code))
+        _IMPL["last"], _IMPL["reason"] = "hip", f"pipelined fork kernel, {pieces} block ranges beside the conv"
+        return {"o0": o0, "ot": ot, "states": states, "tails": tails, "y0": y0, "yt": yt}
     _lib.check(Lb.dllm_conv_fork_fwd(
         r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(bias), y0.data_ptr(), yt.data_ptr(),
         _lib.ptr(tails), B, L, Cd, K, block, code, wcode, cflags, sh), "dllm_conv_fork_fwd")
@@ -289,6 +315,77 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
 
 # kernel names reported through last_impl() for the fused fork (dllm_gdn_state_fork_path)
 _FORK_PATHS = {2: "pipelined fork kernel", 1: "fused fork kernel"}
+
+_CUS: dict = {}
+_SIDE = threading.local()
+
+
+def _device_cus(dev: torch.device) -> int:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _CUS:
+        _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CUS[idx]
+
+
+def fork_workgroups(cus: int, B: int, Hv: int) -> int:
+    """Workgroups of the pipelined fork on a chip of `cus` compute units: one per (sequence, value
+    head), or two (a head's columns split) when those fit in the chip, as the library's dispatch
+    chooses."""
+    return 2 * B * Hv if 2 * B * Hv <= cus else B * Hv
+
+
+def default_pieces(cus: int, B: int, Hv: int, nb: int) -> int:
+    """Block ranges of gdn_state_fork's default schedule: 4 where the conv beside the fork was
+    measured to pay, i.e. one workgroup per head that leaves compute units free and 64 blocks or
+    more (27B-class layer, B = 4, L = 4096: 898 vs 932 us); else 1. Each extra range costs a launch
+    and its pipeline ramp, more than a short conv hides (B = 1, L = 2048 with the column split:
+    277 vs 241 us)."""
+    wgs = fork_workgroups(cus, B, Hv)
+    return 4 if wgs == B * Hv and wgs < cus and nb >= 64 else 1
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """This thread's side stream on `dev` (default priority), created once."""
+    streams = getattr(_SIDE, "streams", None)
+    if streams is None:
+        streams = _SIDE.streams = {}
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in streams:
+        streams[idx] = torch.cuda.Stream(device=idx)
+    return streams[idx]
+
+
+def _launch_ranges(Lb, dev, cuts, conv, fork, dims):
+    """The layer in block ranges [cuts[i], cuts[i+1]): every conv range on this thread's side
+    stream, in order, each followed by an event; each fork range on the current stream after its
+    conv range's event, starting from the snapshot the range before wrote (the kernels' arithmetic
+    per block does not depend on where a launch starts, so the results equal one launch's)."""
+    r0, rt, w, bias, y0, yt, tails, cflags = conv
+    c0, ct, b0, bt_, gg0, ggt, o0, ot, states = fork
+    B, L, Cd, K, Hk, Hv, Dk, Dv, block, code = dims
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev)
+    side.wait_stream(main)  # the inputs as the caller's stream leaves them
+    wcode = _lib.dtype_code(w.dtype)
+    events = []
+    for k0, k1 in zip(cuts, cuts[1:]):
+        _lib.check(Lb.dllm_conv_fork_range_fwd(
+            r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(bias), y0.data_ptr(), yt.data_ptr(), _lib.ptr(tails),
+            B, L, Cd, K, block, code, wcode, cflags, k0, k1, side.cuda_stream), "dllm_conv_fork_range_fwd")
+        ev = torch.cuda.Event()
+        ev.record(side)
+        events.append(ev)
+    for ev, (k0, k1) in zip(events, zip(cuts, cuts[1:])):
+        main.wait_event(ev)
+        _lib.check(Lb.dllm_gdn_state_fork_range_fwd(
+            c0.data_ptr(), ct.data_ptr(), L * Cd, Cd, b0.data_ptr(), bt_.data_ptr(), gg0.data_ptr(), ggt.data_ptr(),
+            o0.data_ptr(), ot.data_ptr(), _lib.ptr(states), B, L, Hk, Hv, Dk, Dv, block, code, Dk ** -0.5, k0, k1,
+            main.cuda_stream), "dllm_gdn_state_fork_range_fwd")
+    # every side-stream launch is joined into the caller's stream above; the caching allocator is
+    # told of the side stream's use all the same
+    for t in (r0, rt, w, bias, y0, yt, tails):
+        if t is not None:
+            t.record_stream(side)
 
 
 def kernel_status(reset: bool = True) -> int:
@@ -417,27 +514,8 @@ class StateForkPlan:
         else:
             pieces = max(1, min(int(pieces), nb))
             cuts = [nb * i // pieces for i in range(pieces + 1)]
-        pieces = len(cuts) - 1
-        if not hasattr(self, "_side"):
-            self._side = torch.cuda.Stream(device=self.device)
-            self._events = []
-        while len(self._events) < pieces:
-            self._events.append(torch.cuda.Event())
-        main = torch.cuda.current_stream(self.device)
-        bounds = list(zip(cuts, cuts[1:]))
-        wc = _lib.dtype_code(self.w.dtype)
-        self._side.wait_stream(main)
-        for i, (k0, k1) in enumerate(bounds):
-            _lib.check(self._lib.dllm_conv_fork_range_fwd(
-                self.raw0.data_ptr(), self.rawt.data_ptr(), self.w.data_ptr(), None, self.y0.data_ptr(),
-                self.yt.data_ptr(), _lib.ptr(self.tails), B, L, Cd, self.K, block, self.code, wc, 0, k0, k1,
-                self._side.cuda_stream), "dllm_conv_fork_range_fwd")
-            self._events[i].record(self._side)
-        for i, (k0, k1) in enumerate(bounds):
-            main.wait_event(self._events[i])
-            _lib.check(self._lib.dllm_gdn_state_fork_range_fwd(
-                self.y0.data_ptr(), self.yt.data_ptr(), L * Cd, Cd, self.beta0.data_ptr(), self.betat.data_ptr(),
-                self.g0.data_ptr(), self.gt.data_ptr(), self.o0.data_ptr(), self.ot.data_ptr(),
-                _lib.ptr(self.states), B, L, Hk, Hv, Dk, Dv, block, self.code, Dk ** -0.5, k0, k1,
-                main.cuda_stream), "dllm_gdn_state_fork_range_fwd")
+        _launch_ranges(self._lib, self.device, cuts,
+                       (self.raw0, self.rawt, self.w, None, self.y0, self.yt, self.tails, 0),
+                       (self.y0, self.yt, self.beta0, self.betat, self.g0, self.gt, self.o0, self.ot, self.states),
+                       (B, L, Cd, self.K, Hk, Hv, Dk, Dv, block, self.code))
         _IMPL["last"], _IMPL["reason"] = "hip", ""

@@ -1,0 +1,26 @@
+"""Host-side choices of the state-fork layer that need no GPU."""
+
+from dllm_qwen38_amd import gdn
+
+
+def test_fork_workgroups_rule():
+    """One workgroup per (sequence, value head), or two when twice that fits in the chip; the
+    default schedule puts the conv beside the fork only when this leaves compute units free."""
+    cus = 256
+    assert gdn.fork_workgroups(cus, 4, 48) == 192       # 27B-class layer: 64 CUs free
+    assert gdn.fork_workgroups(cus, 8, 16) == 256       # 0.8B-class layer: split, chip full
+    assert gdn.fork_workgroups(cus, 1, 48) == 96        # one sequence of the 27B stack: split
+    assert gdn.fork_workgroups(cus, 8, 48) == 384       # more heads than CUs: no split
+    assert gdn.fork_workgroups(cus, 2, 64) == 256
+    assert gdn.fork_workgroups(cus, 3, 43) == 129       # 2 * 129 > 256: one per head
+
+
+def test_default_pieces_rule():
+    """Block ranges by default only where they were measured to pay: one workgroup per head with
+    compute units left free, and at least 64 blocks."""
+    cus = 256
+    assert gdn.default_pieces(cus, 4, 48, 128) == 4   # 27B-class layer, L = 4096
+    assert gdn.default_pieces(cus, 4, 48, 32) == 1    # too few blocks per range
+    assert gdn.default_pieces(cus, 1, 48, 64) == 1    # column split (96 workgroups)
+    assert gdn.default_pieces(cus, 8, 16, 64) == 1    # column split fills the chip
+    assert gdn.default_pieces(cus, 8, 48, 128) == 1   # 384 workgroups: no CU free

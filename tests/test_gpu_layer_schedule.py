@@ -104,3 +104,57 @@ def test_column_split_of_the_fork_is_bit_identical(dev, shape, B, L):
         assert torch.equal(got[1][k], got[2][k]), k
     assert lib.dllm_set_fork_split(3) == -1
     assert gdn.kernel_status(reset=True) == 0
+
+
+def _fork(x, s, **kw):
+    return gdn.gdn_state_fork(x["raw0"], x["rawt"], x["conv_w"], x["beta0"], x["betat"], x["g0"], x["gt"],
+                              num_k_heads=s.Hk, num_v_heads=s.Hv, head_k_dim=s.D, head_v_dim=s.D, block=s.block, **kw)
+
+
+@pytest.mark.parametrize("shape,B,L", [("GDN_27B_BF16", 1, 512), ("GDN_08B_BF16", 2, 1024),
+                                       ("GDN_27B_BF16", 4, 2048)])
+def test_state_fork_api_schedules_are_bit_identical(dev, shape, B, L):
+    """gdn_state_fork with its default schedule, explicit range counts and one launch: identical
+    outputs, conv tails and snapshots, with a conv bias and under the no-conv-prefix fault too."""
+    s = getattr(inputs, shape)
+    x = {k: v.to(dev) for k, v in inputs.gdn_layer_inputs(s, B=B, L=L, g_shift=-4.0).items()}
+    g = torch.Generator().manual_seed(5)
+    bias = (torch.rand(x["conv_w"].shape[0], generator=g) - 0.5).to(x["conv_w"].dtype).to(dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    auto_ranges = gdn.default_pieces(cus, B, s.Hv, L // s.block) > 1
+    for kw in ({}, {"conv_bias": bias}, {"fault": "no-conv-prefix"}):
+        ref = _fork(x, s, pieces=1, **kw)
+        torch.cuda.synchronize()
+        assert "block ranges" not in gdn.last_impl()[1]
+        ref = {k: v.clone() for k, v in ref.items() if v is not None}
+        for pieces in (None, 2, 3, 7):
+            print(f"{shape} B={B} L={L} {sorted(kw)} pieces={pieces}", flush=True)
+            got = _fork(x, s, pieces=pieces, **kw)
+            torch.cuda.synchronize()
+            ranges = pieces is not None or auto_ranges
+            assert ("block ranges" in gdn.last_impl()[1]) == ranges, (pieces, gdn.last_impl())
+            for k in ref:
+                assert torch.equal(got[k], ref[k]), (kw, pieces, k)
+    assert gdn.kernel_status(reset=True) == 0
+
+
+def test_state_fork_api_schedule_arguments(dev):
+    """Block ranges need the snapshots and the pipelined kernel: without them the default is one
+    launch and an explicit range count is refused."""
+    s = inputs.GDN_27B_BF16
+    x = {k: v.to(dev) for k, v in inputs.gdn_layer_inputs(s, B=1, L=256).items()}
+    with pytest.raises(ValueError, match="pieces"):
+        _fork(x, s, pieces=0)
+    with pytest.raises(ValueError, match="states"):
+        _fork(x, s, pieces=2, need_states=False)
+    r = _fork(x, s, need_states=False)
+    torch.cuda.synchronize()
+    assert r["states"] is None and "block ranges" not in gdn.last_impl()[1]
+    t = inputs.GDN_TINY_F32
+    xt = {k: v.to(dev) for k, v in inputs.gdn_layer_inputs(t).items()}
+    with pytest.raises(ValueError, match="pipelined"):
+        _fork(xt, t, pieces=2)
+    _fork(xt, t)
+    torch.cuda.synchronize()
+    assert "block ranges" not in gdn.last_impl()[1]
+    assert gdn.kernel_status(reset=True) == 0

@@ -265,7 +265,9 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     wcode = _lib.dtype_code(w.dtype)
     cflags = 1 if fault == "no-conv-prefix" else 0
     bias = None if conv_bias is None else conv_bias.contiguous()
-    ranges_ok = states is not None and nb >= 2 and Lb.dllm_gdn_state_fork_path(Dk, Dv, block, code) == 2
+    # block ranges run on the pipelined kernel, which reads 16-byte rows of the conv outputs
+    ranges_ok = (states is not None and nb >= 2 and Lb.dllm_gdn_state_fork_path(Dk, Dv, block, code) == 2
+                 and y0.data_ptr() % 16 == 0 and yt.data_ptr() % 16 == 0)
     if pieces is None:
         pieces = default_pieces(_device_cus(dev), B, Hv, nb) if ranges_ok else 1
     pieces = int(pieces)

@@ -109,7 +109,7 @@ def main(argv=None):
     a = ap.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the state-fork layer shards over (batch, value head) with no "
-              "exchange, and this build runs and reports the single-GPU share; use --gpus 1", file=sys.stderr)
+              "exchange, and bench.py runs and reports the single-GPU share; use --gpus 1", file=sys.stderr)
         return 2
     if a.workload == "attention":
         return bench_attention(a)

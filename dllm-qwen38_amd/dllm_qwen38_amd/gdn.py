@@ -25,10 +25,10 @@ _IMPL = {"force": None, "last": "hip", "reason": ""}
 
 
 def set_impl(name):
-    """'hip' | None. The reference also accepts 'torch' / 'fla'; this build has only the HIP core,
-    so forcing anything else raises (gdn.py:39-41, 158-159)."""
+    """'hip' | None. The reference also accepts 'torch' / 'fla'; this package has only the HIP
+    core, so forcing anything else raises (gdn.py:39-41, 158-159)."""
     if name not in (None, "hip"):
-        raise RuntimeError(f"{name} forced but unavailable: this build runs the HIP core only")
+        raise RuntimeError(f"{name} forced but unavailable: this package runs the HIP core only")
     _IMPL["force"] = name
 
 

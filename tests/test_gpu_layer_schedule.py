@@ -7,6 +7,8 @@ where a launch starts. Slow decay (g shift -4) keeps the carried state visible i
 Also the range entry points' argument checks (a range after block 0 needs the states tensor;
 ranges need the pipelined kernel; the range must lie inside the sequence)."""
 
+import dataclasses
+
 import pytest
 import torch
 
@@ -157,4 +159,35 @@ def test_state_fork_api_schedule_arguments(dev):
     _fork(xt, t)
     torch.cuda.synchronize()
     assert "block ranges" not in gdn.last_impl()[1]
+    assert gdn.kernel_status(reset=True) == 0
+
+
+@pytest.mark.parametrize("block", [16, 8])
+def test_ranges_at_subtile_blocks_are_bit_identical(dev, block):
+    """Blocks shorter than the kernel's 32-row tile (rows past the block are padding) in block
+    ranges: the plan's overlapped schedule and the drop-in's explicit ranges equal one launch."""
+    s = dataclasses.replace(inputs.GDN_27B_BF16, block=block)
+    B, L = 1, 256
+    nb = L // block
+    p = _plan(dev, s, B, L, g_shift=-4.0)
+    assert p.overlap_supported()
+    p.run()
+    torch.cuda.synchronize()
+    ref = {k: getattr(p, k).clone() for k in OUTS}
+    for kw in ({"pieces": 3}, {"bounds": [0, 1, nb // 2 + 1, nb]}):
+        for k in OUTS:
+            getattr(p, k).fill_(float("nan"))
+        print(f"block={block} run_overlapped({kw})", flush=True)
+        p.run_overlapped(**kw)
+        torch.cuda.synchronize()
+        for k in OUTS:
+            assert torch.equal(getattr(p, k), ref[k]), (kw, k)
+    x = {k: v.to(dev) for k, v in inputs.gdn_layer_inputs(s, B=B, L=L, g_shift=-4.0).items()}
+    one = _fork(x, s, pieces=1)
+    torch.cuda.synchronize()
+    one = {k: v.clone() for k, v in one.items() if v is not None}
+    got = _fork(x, s, pieces=5)
+    torch.cuda.synchronize()
+    for k in one:
+        assert torch.equal(got[k], one[k]), k
     assert gdn.kernel_status(reset=True) == 0

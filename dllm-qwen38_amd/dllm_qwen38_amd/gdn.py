@@ -89,6 +89,13 @@ def chunk_gated_delta_rule_with_states(
     out = torch.empty(B, T, Hv, Dv, dtype=dt, device=dev)
     states = (torch.empty(B, T // chunk_size, Hv, Dk, Dv, dtype=torch.float32, device=dev)
               if need_states else None)
+    if B == 0 or T == 0:
+        # nothing to compute; as the reference, an empty sequence has no chunk states to stack
+        # (its torch.stack of an empty list raises, gdn.py:123)
+        if T == 0 and need_states:
+            raise RuntimeError("chunk_gated_delta_rule_with_states: a sequence of length 0 has no chunk states")
+        _IMPL["last"], _IMPL["reason"] = "hip", "empty input"
+        return out, states
     L = _lib.lib()
     _lib.check(L.dllm_gdn_chunk_fwd(
         q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
@@ -139,11 +146,12 @@ def causal_conv1d_fn(hidden_states: torch.Tensor, weight: torch.Tensor, bias: to
     if pre is not None and (pre.shape[0] != B or pre.shape[1] != C):
         raise ValueError(f"conv_prefix must be [B, C, P] = [{B}, {C}, P], got {tuple(pre.shape)}")
     L = _lib.lib()
-    _lib.check(L.dllm_causal_conv1d_fwd(
-        x.data_ptr(), _lib.strides3(x), _lib.ptr(pre), None if pre is None else _lib.strides3(pre),
-        0 if pre is None else pre.shape[2], w.data_ptr(), _lib.ptr(b), y.data_ptr(), B, C, T, K,
-        _lib.dtype_code(x.dtype), _lib.dtype_code(w.dtype), int(activation is not None), _lib.stream_handle(dev)),
-        "dllm_causal_conv1d_fwd")
+    if B > 0 and T > 0 and C > 0:  # an empty input has an empty output (no launch)
+        _lib.check(L.dllm_causal_conv1d_fwd(
+            x.data_ptr(), _lib.strides3(x), _lib.ptr(pre), None if pre is None else _lib.strides3(pre),
+            0 if pre is None else pre.shape[2], w.data_ptr(), _lib.ptr(b), y.data_ptr(), B, C, T, K,
+            _lib.dtype_code(x.dtype), _lib.dtype_code(w.dtype), int(activation is not None),
+            _lib.stream_handle(dev)), "dllm_causal_conv1d_fwd")
     if not return_final_states:
         return y.transpose(1, 2)
     xin = x if pre is None else torch.cat([pre.to(x.dtype), x], 2)

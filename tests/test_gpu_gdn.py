@@ -191,3 +191,32 @@ def test_state_fork_27b_full_size_properties(dev):
         d = _maxabs(o, ota[:, sl])
         print(f"noised block {kb}: relaunch max|d| = {d:.3e} (bit-equal: {torch.equal(o, ota[:, sl])})")
         assert d <= BF16_OUT_ATOL, f"noised block {kb} differs from its relaunch"
+
+
+def test_empty_inputs_follow_the_reference(dev):
+    """Empty batches and sequences launch nothing: outputs (and states) of the right shapes, as the
+    reference's torch path returns them; a sequence of length 0 with states requested raises, as
+    the reference's stack of an empty list of chunk states does (gdn.py:123)."""
+    Hk, Hv, D = 2, 4, 64
+    mk = lambda B, T, H: torch.randn(B, T, H, D, device=dev)
+    gz = lambda B, T: -torch.rand(B, T, Hv, device=dev)
+    o, st = gdn.chunk_gated_delta_rule_with_states(mk(0, 64, Hk), mk(0, 64, Hk), mk(0, 64, Hv), gz(0, 64),
+                                                   torch.rand(0, 64, Hv, device=dev), chunk_size=32)
+    assert o.shape == (0, 64, Hv, D) and st.shape == (0, 2, Hv, D, D) and st.dtype == torch.float32
+    o, st = gdn.chunk_gated_delta_rule_with_states(mk(2, 0, Hk), mk(2, 0, Hk), mk(2, 0, Hv), gz(2, 0),
+                                                   torch.rand(2, 0, Hv, device=dev), chunk_size=32, need_states=False)
+    assert o.shape == (2, 0, Hv, D) and st is None
+    with pytest.raises(RuntimeError, match="length 0"):
+        gdn.chunk_gated_delta_rule_with_states(mk(2, 0, Hk), mk(2, 0, Hk), mk(2, 0, Hv), gz(2, 0),
+                                               torch.rand(2, 0, Hv, device=dev), chunk_size=32)
+    w = torch.randn(16, 4, device=dev)
+    y = gdn.causal_conv1d_fn(torch.randn(3, 16, 0, device=dev), w, activation="silu")
+    assert y.shape == (3, 16, 0)
+    y = gdn.causal_conv1d_fn(torch.randn(0, 16, 8, device=dev), w, activation="silu")
+    assert y.shape == (0, 16, 8)
+    # the final states of an empty segment are the last K-1 inputs of its prefix
+    pre = torch.randn(3, 16, 3, device=dev)
+    y, fin = gdn.causal_conv1d_fn(torch.randn(3, 16, 0, device=dev), w, activation="silu", initial_states=pre,
+                                  return_final_states=True)
+    assert y.shape == (3, 16, 0) and torch.equal(fin, pre)
+    torch.cuda.synchronize()

@@ -66,6 +66,8 @@ def bd_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: in
         out = torch.empty(B, S, Hq, d, dtype=q.dtype, device=dev)
     elif tuple(out.shape) != (B, S, Hq, d) or not out.is_contiguous() or out.dtype != q.dtype:
         raise ValueError("out must be a contiguous [B, 2L, Hq, d] tensor of q's dtype")
+    if B == 0 or L == 0:  # no queries: an empty output, no launch
+        return out
     sc = d ** -0.5 if scale is None else float(scale)
     _lib.check(_lib.lib().dllm_bd_attention_fwd(
         q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
@@ -111,6 +113,8 @@ def block_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         out = torch.empty(B, M, Hq, d, dtype=q.dtype, device=dev)
     elif tuple(out.shape) != (B, M, Hq, d) or not out.is_contiguous() or out.dtype != q.dtype:
         raise ValueError("out must be a contiguous [B, M, Hq, d] tensor of q's dtype")
+    if B == 0 or M == 0:  # no queries: an empty output, no launch
+        return out
     sc = d ** -0.5 if scale is None else float(scale)
     ks = _key_splits(q, M, N, d) if key_splits is None else int(key_splits)
     work = torch.empty(ks * B * M * Hq * (d + 2), dtype=torch.float32, device=dev) if ks > 1 else None

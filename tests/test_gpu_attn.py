@@ -115,3 +115,16 @@ def test_27b_attention_shape_sampled_rows_and_determinism(dev):
         sc = sc.masked_fill(~allowed[r][None, None], float("-inf"))
         ref = torch.einsum("bhj,bjhd->bhd", torch.softmax(sc, -1), vx)
         _check(o1[:, r], ref, torch.bfloat16, f"27B-class attention row {r}", v.float().abs().max().item())
+
+
+def test_empty_queries_give_empty_outputs(dev):
+    """No queries (empty batch or sequence): an empty output of the right shape, no launch, as the
+    reference's eager attention returns for an empty score matrix."""
+    for B, L in ((0, 64), (2, 0)):
+        q = torch.randn(B, 2 * L, 4, 64, device=dev, dtype=torch.bfloat16)
+        k = torch.randn(B, 2 * L, 2, 64, device=dev, dtype=torch.bfloat16)
+        assert attention.bd_attention(q, k, k, block=32).shape == (B, 2 * L, 4, 64)
+    q = torch.randn(2, 0, 4, 64, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(2, 96, 2, 64, device=dev, dtype=torch.bfloat16)
+    assert attention.block_causal_attention(q, k, k, block=32, q_offset=64).shape == (2, 0, 4, 64)
+    torch.cuda.synchronize()

@@ -45,6 +45,8 @@ def _check(got, ref, dtype, name, vmax=None):
     (1, 200, 6, 1, 256, 8),    # d = 256, six query heads on one K/V head, ragged L, element masks
     (3, 160, 4, 2, 256, 16),   # d = 256, query groups crossing blocks, B = 3
     (1, 72, 2, 1, 128, 24),    # a block that is not a divisor of the 32-key tile
+    (1, 256, 4, 2, 256, 64),   # blocks longer than the 32-key tile
+    (2, 192, 4, 1, 128, 64),
 ])
 def test_bd_attention_matches_oracle(dev, dtype, B, L, Hq, Hkv, d, block):
     q, k, v = _inputs(B, L, Hq, Hkv, d, dtype, seed=L + d + block)

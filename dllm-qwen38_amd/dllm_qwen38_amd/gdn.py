@@ -347,7 +347,7 @@ def fork_workgroups(cus: int, B: int, Hv: int) -> int:
 def default_pieces(cus: int, B: int, Hv: int, nb: int) -> int:
     """Block ranges of gdn_state_fork's default schedule: 4 where the conv beside the fork was
     measured to pay, i.e. one workgroup per head that leaves compute units free and 64 blocks or
-    more (27B-class layer, B = 4, L = 4096: 898 vs 932 us); else 1. Each extra range costs a launch
+    more (27B-class layer, B = 4, L = 4096: 850 vs 861 us); else 1. Each extra range costs a launch
     and its pipeline ramp, more than a short conv hides (B = 1, L = 2048 with the column split:
     277 vs 241 us)."""
     wgs = fork_workgroups(cus, B, Hv)

@@ -26,6 +26,7 @@ extern "C" int dllm_fork_layout(int B, int L, int block, int width, int32_t* row
   if (B <= 0 || L <= 0 || block <= 0 || width < 1) return fail(DLLM_EINVAL, "fork layout: bad sizes");
   if (L % block) return fail(DLLM_EINVAL, "L=%d is not a multiple of block=%d", L, block);
   const int nb = L / block;
+  if ((long long)B * nb > 0x7fffffffLL) return fail(DLLM_EUNSUPPORTED, "fork layout: %d x %d fork rows", B, nb);
   const int n = B * nb;
   fork_layout_kernel<<<(n + 255) / 256, 256, 0, (hipStream_t)stream>>>(B, nb, block, width, row, state_src,
                                                                        prefix_pos);

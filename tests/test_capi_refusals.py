@@ -181,6 +181,8 @@ CASES = {
     # fork layout (src/dllm_qwen38/blockdiff.py:161-177)
     "layout prefix missing": (("dllm_fork_layout", 1, 64, 32, 4, P, P, None, None), EINVAL, "fork layout: null pointer"),
     "layout width 0": (("dllm_fork_layout", 1, 64, 32, 0, P, P, P, None), EINVAL, "fork layout: bad sizes"),
+    "layout rows past 32 bits": (("dllm_fork_layout", 1 << 16, 1 << 20, 16, 4, P, P, P, None), EUNSUP,
+                                 "65536 x 65536 fork rows"),
 }
 
 

@@ -5,9 +5,9 @@ inherits is ~1e-11 of its own contribution and a wrong carry would not show. The
 the same kernels with slow decay, g = -softplus(N(0,1) - 4) (about 0.9 nats per block), over 32
 blocks, and compare with the fp32 oracle on the same bf16 inputs within the bounds of
 tests/_bounds.py (which a dropped, mis-scaled or mis-forked carry exceeds: tests/test_oracle_gdn.py).
-They cover the pipelined fork kernel at both head layouts, at blocks 32, 16 and 8 and without
-state snapshots, and the bf16 chunk kernel (one and two column windows per head) with an
-initial state.
+They cover the pipelined fork kernel at both head layouts, at blocks 32, 16 and 8, without
+state snapshots and at grids that are not a multiple of the 8 XCDs or exceed the chip's CUs, and
+the bf16 chunk kernel (one and two column windows per head) with an initial state.
 """
 
 import numpy as np
@@ -93,6 +93,23 @@ def test_pipe_fork_subtile_blocks(dev, block):
     _check(f"block {block} o0", r["o0"], o0, out_bound)
     _check(f"block {block} ot", r["ot"], ot, out_bound)
     _check(f"block {block} states", r["states"], st, state_bound)
+
+
+@pytest.mark.parametrize("B,Hk,Hv,L", [(3, 1, 5, 128), (5, 1, 53, 64)], ids=["30 workgroups", "265 workgroups"])
+def test_pipe_fork_grids_not_a_multiple_of_eight(dev, B, Hk, Hv, L):
+    """Workgroup counts that are not a multiple of the 8 XCDs (the kernel maps dispatch slots to
+    (sequence, head) pairs per XCD; every pair must still be reached exactly once) and more
+    workgroups than the chip has CUs (several rounds): 15 heads with their columns split over two
+    workgroups (30), and 265 heads one workgroup each."""
+    s = _shape(f"B {B}, Hk {Hk}, Hv {Hv}", B, L, 32, Hk, Hv, 8150 + Hv)
+    x = inputs.gdn_layer_inputs(s)
+    r = _fork(s, x, dev)
+    assert gdn.last_impl()[0] == "hip" and gdn.last_impl()[1].startswith("pipelined fork kernel")
+    o0, ot, st, tails = _oracle(s, x)
+    assert torch.equal(r["tails"], tails)
+    _check(f"{B}x{Hv} o0", r["o0"], o0, out_bound)
+    _check(f"{B}x{Hv} ot", r["ot"], ot, out_bound)
+    _check(f"{B}x{Hv} states", r["states"], st, state_bound)
 
 
 def test_pipe_fork_need_states_false_is_bit_identical(dev):

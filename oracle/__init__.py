@@ -2,7 +2,7 @@
 
 This package restates, on the CPU, the reference algorithm of `kotoba-lang/dllm-qwen38`'s
 block-diffusion forward (the state-fork Gated DeltaNet layer, its causal short conv with
-conv-prefix carry-in, and the complementary-mask attention). It is the checker the HIP
+conv-prefix carry-in, and the complementary-mask attention). It is the oracle the HIP
 kernels are compared against; it is never the thing measured or shipped.
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import

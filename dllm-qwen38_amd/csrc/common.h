@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dllm_hip.h"  // every entry point's definition is checked against its declaration
+
 namespace dllm {
 
 typedef __bf16 bf16;

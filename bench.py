@@ -297,7 +297,7 @@ def bench_attention(a):
                                "cat([x_t, x_0]), bf16", "global_batch": B, "seq_len": L, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": tf / BF16_MFMA_PEAK_TFLOPS,
-                     "traffic": _traffic_from_profiles("attention_config4_traffic.json")},
+                     "traffic": _traffic_from_profiles("attention_27b_traffic.json")},
         "algorithmic_gflop": fl / 1e9, "wall_s_timed": wall, "cpu_baseline": None,
     }
     _calibration_copy(a, dev)

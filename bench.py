@@ -100,9 +100,11 @@ def main(argv=None):
                          "with the conv of each range beside the fork of the one before (1 = conv, then fork; "
                          "default 4 at the 27B-class shape, 1 at the 0.8B-class shape, where it measured no gain)")
     ap.add_argument("--workload", default="gdn-layer",
-                    choices=["gdn-layer", "gdn-layer-08b", "attention", "stack", "decode"],
+                    choices=["gdn-layer", "gdn-layer-08b", "gdn-core", "attention", "stack", "decode"],
                     help="gdn-layer (default, the headline metric); gdn-layer-08b: the same layer at the 0.8B-class "
-                         "shape (B=8 L=2048 Hk=Hv=16 D=128); attention: the complementary-mask attention "
+                         "shape (B=8 L=2048 Hk=Hv=16 D=128); gdn-core: the chunked gated delta rule with "
+                         "per-chunk states on the 27B-class clean stream (B=4 T=4096); attention: the "
+                         "complementary-mask attention "
                          "layer kernel at B=2 L=4096 Hq=24 Hkv=4 d=256; stack: the 16-layer 27B-class "
                          "two-stream forward at B=1 L=2048; decode: one cached denoising step of that stack "
                          "(a 32-token block over a 2048-token clean prefix)")
@@ -113,6 +115,8 @@ def main(argv=None):
         return 2
     if a.workload == "attention":
         return bench_attention(a)
+    if a.workload == "gdn-core":
+        return bench_gdn_core(a)
     if a.workload in ("stack", "decode"):
         # the library GEMMs around the path use the committed TunableOp solution table
         from dllm_qwen38_amd import gemm_tuning
@@ -268,6 +272,64 @@ def _timed(fn, steps, warmup, stream):
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
+
+
+def bench_gdn_core(a):
+    """chunk_gated_delta_rule_with_states (reference gdn.py:48-123) as the clean pass of the 27B-class
+    fork calls it (blockdiff.py:160): B=4 T=4096 chunk 32, Hk=16 Hv=48 Dk=Dv=128, bf16 q/k/v (q and k
+    on their 16 key heads, GQA by indexing), fp32 g and beta, the fp32 state after every chunk kept.
+    Roofline: HBM, on q, k, v, g and beta read once and the output and states written once."""
+    import torch
+
+    from dllm_qwen38_amd import gdn, inputs
+
+    B, T, Hk, Hv, D, C = 4, 4096, 16, 48, 128, 32
+    dev = torch.device("cuda:0")
+    q, k, v, g, beta = inputs.gdn_core_inputs(B, T, Hk, Hv, D, torch.bfloat16, seed=300, g_shift=1.0)
+    qd, kd, vd, gd, bd = (t.to(dev) for t in (q, k, v, g, beta))
+    stream = torch.cuda.current_stream(dev)
+    ms, wall = _timed(lambda: gdn.chunk_gated_delta_rule_with_states(qd, kd, vd, gd, bd, C), a.steps, a.warmup, stream)
+    nbytes = (2 * B * T * Hk * D + B * T * Hv * D) * 2 + 2 * B * T * Hv * 4 + B * T * Hv * D * 2 \
+        + B * (T // C) * Hv * D * D * 4
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    res = {
+        "metric": "chunked gated delta rule tokens/s (B*T positions) at the 27B-class shape; % HBM roofline",
+        "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q, k, v; sigmoid beta; g = -softplus(N(0,1) + 1))",
+        "config": {"workload": "chunked gated delta rule with per-chunk states, B=4 T=4096 chunk 32 Hk=16 Hv=48 "
+                               "Dk=Dv=128, bf16 in/out, fp32 state", "global_batch": B, "seq_len": T,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "gdn_chunk_kernel",
+                     "algorithmic_bytes": nbytes},
+        "wall_s_timed": wall, "cpu_baseline": None,
+    }
+    if not a.no_cpu_baseline:
+        sys.path.insert(0, ROOT)
+        from oracle import gdn_ref
+
+        n = len(os.sched_getaffinity(0))
+        torch.set_num_threads(n)
+        Ts = T
+        qs, ks, vs, gs, bs = (t[:1, :Ts] for t in (q, k, v, g, beta))
+        # the oracle takes q and k on the value heads, as the reference's mixer expands them (gdn.py:227-229)
+        qs, ks = qs.repeat_interleave(Hv // Hk, 2), ks.repeat_interleave(Hv // Hk, 2)
+        gdn_ref.chunk_gated_delta_rule_with_states(qs, ks, vs, gs, bs, C)
+        times = []
+        start = time.perf_counter()
+        while len(times) < 3 or time.perf_counter() - start < a.cpu_budget_s:
+            t0 = time.perf_counter()
+            gdn_ref.chunk_gated_delta_rule_with_states(qs, ks, vs, gs, bs, C)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        res["cpu_baseline"] = {"value": Ts / med, "unit": "tokens/s", "cores": n, "kind": "port",
+                               "sample": f"B=1 T={Ts} (one sequence of the workload), same heads, "
+                                         f"bf16-rounded inputs, fp32 torch CPU oracle; median of {len(times)} runs "
+                                         f"({med:.2f} s/run)", **_host_info()}
+        res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
+    print(json.dumps(res))
+    return 0
 
 
 def bench_attention(a):

@@ -7,7 +7,9 @@ blocks, and compare with the fp32 oracle on the same bf16 inputs within the boun
 tests/_bounds.py (which a dropped, mis-scaled or mis-forked carry exceeds: tests/test_oracle_gdn.py).
 They cover the pipelined fork kernel at both head layouts, at blocks 32, 16 and 8, without
 state snapshots and at grids that are not a multiple of the 8 XCDs or exceed the chip's CUs, and
-the bf16 chunk kernel (one and two column windows per head) with an initial state.
+the bf16 chunked rule with an initial state on both of its kernels (the pipelined kernel on one
+stream for chunks that divide the tile, the chunk kernel with one and two column windows per head
+for longer chunks).
 """
 
 import numpy as np
@@ -123,12 +125,14 @@ def test_pipe_fork_need_states_false_is_bit_identical(dev):
     assert torch.equal(a["o0"], b["o0"]) and torch.equal(a["ot"], b["ot"])
 
 
-@pytest.mark.parametrize("B,Hk,Hv", [(1, 2, 8), (2, 16, 64)], ids=["two-windows", "one-window"])
-@pytest.mark.parametrize("chunk", [32, 64])
+@pytest.mark.parametrize("B,Hk,Hv", [(1, 2, 8), (2, 16, 64), (3, 16, 48)], ids=["8 heads", "128 heads", "144 heads"])
+@pytest.mark.parametrize("chunk", [32, 16, 64])
 def test_chunk_kernel_bf16_matches_oracle(dev, B, Hk, Hv, chunk):
     """chunk_gated_delta_rule_with_states in bf16 at Dk = Dv = 128 with an initial state and slow
-    decay: fewer than 128 (sequence, head) pairs run two 64-column windows per head, more run one
-    128-column window (the decoder and the two-pass fork use both)."""
+    decay. Chunks of 32 and 16 run the pipelined kernel on one stream (a head's columns over two
+    workgroups up to 128 (sequence, head) pairs on this chip, one workgroup each above); chunks of
+    64 run the chunk kernel (two 64-column windows per head below 128 pairs, one 128-column window
+    from 128)."""
     T = 512
     q, k, v, g, beta = inputs.gdn_core_inputs(B, T, Hk, Hv, 128, torch.bfloat16, seed=7150 + Hv + chunk,
                                               g_shift=SLOW)

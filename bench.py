@@ -301,7 +301,7 @@ def bench_gdn_core(a):
                                "Dk=Dv=128, bf16 in/out, fp32 state", "global_batch": B, "seq_len": T,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "gdn_chunk_kernel",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "gdn_fork_pipe_kernel<.., 1> (one stream)",
                      "algorithmic_bytes": nbytes},
         "wall_s_timed": wall, "cpu_baseline": None,
     }

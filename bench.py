@@ -69,7 +69,7 @@ def cpu_baseline(s, sample_L: int, budget_s: float):
     x = inputs.gdn_layer_inputs(s, B=1, L=sample_L)
     args = (x["raw0"], x["rawt"], x["conv_w"], x["beta0"], x["betat"], x["g0"], x["gt"])
     kw = dict(Hk=s.Hk, Hv=s.Hv, Dk=s.D, Dv=s.D, block=s.block)
-    gdn_ref.state_fork_layer(*args, **kw)  # warm-up
+    ref = gdn_ref.state_fork_layer(*args, **kw)  # warm-up
     times = []
     start = time.perf_counter()
     while len(times) < 3 or time.perf_counter() - start < budget_s:
@@ -79,9 +79,54 @@ def cpu_baseline(s, sample_L: int, budget_s: float):
     med = statistics.median(times)
     return {"value": sample_L / med, "unit": "tokens/s", "cores": n, "kind": "port",
             "sample": f"one sequence (B=1 L={sample_L}) of the workload's shape (Hk={s.Hk} Hv={s.Hv} D={s.D} "
-                      f"block {s.block}), bf16-rounded inputs, fp32 torch CPU oracle on {n} threads; median of "
-                      f"{len(times)} runs after 1 warm-up ({med:.2f} s/run, {sum(times):.1f} s timed)",
-            **_host_info()}
+                    f"block {s.block}): the workload's own sequence 0, bf16-rounded inputs, fp32 torch CPU oracle "
+                    f"on {n} threads; median of {len(times)} runs after 1 warm-up ({med:.2f} s/run, min "
+                    f"{min(times):.2f} s, {sum(times):.1f} s timed)",
+            **_host_info()}, (x, ref)
+
+
+def _err_stats(got, ref, bound):
+    """max / mean / 99th and 99.9th percentile of |got - ref|, and the largest |d| / bound."""
+    import torch
+
+    d = (got.float() - ref.float()).abs().flatten()
+    n = d.numel()
+    q = lambda f: d.kthvalue(max(1, min(n, int(round(f * n))))).values.item()
+    return {"max": d.max().item(), "mean": d.mean().item(), "p99": q(0.99), "p999": q(0.999),
+            "max_over_bound": (d / bound(ref).flatten()).max().item(), "max_ref": ref.float().abs().max().item()}
+
+
+def parity_sample(plan, s, sample, f64_heads: int = 8):
+    """The GPU outputs of sequence 0 against the CPU oracle run on the same inputs (the cpu_baseline
+    sample is the workload's own sequence 0), with the error distribution: both output streams and
+    every state snapshot against the fp32 oracle, and the clean stream's outputs and snapshots of the
+    first `f64_heads` value heads against the float64 token recurrence. The bound of each figure is
+    the tests' bf16 bound (outputs 2^-6 max|ref| + 2^-7 |ref|, fp32 states 2^-7 max|ref|); a
+    max_over_bound at or below 1 is within it."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import gdn_ref
+
+    u = 2.0 ** -8
+    out_b = lambda r: 4 * u * r.float().abs().max() + 2 * u * r.float().abs()
+    st_b = lambda r: (2 * u * r.float().abs().max()).expand_as(r.float())
+    x, (o0, ot, st, _) = sample
+    Ls = o0.shape[1]
+    g0, gt, gs = plan.o0[:1, :Ls].cpu(), plan.ot[:1, :Ls].cpu(), plan.states[:1, :Ls // s.block].cpu()
+    res = {"sample": f"sequence 0, L={Ls}, all {s.Hv} value heads, against the fp32 CPU oracle; clean stream heads "
+                     f"0-{f64_heads - 1} against the float64 token recurrence",
+           "o0": _err_stats(g0, o0, out_b), "ot": _err_stats(gt, ot, out_b), "states": _err_stats(gs, st, st_b)}
+    y = gdn_ref.causal_conv1d(x["raw0"].transpose(1, 2), x["conv_w"]).transpose(1, 2)
+    q, k, v = gdn_ref._split_heads(y, 1, Ls, s.Hk, s.Hv, s.D, s.D)
+    hs = slice(0, f64_heads)
+    fo, fs = gdn_ref.recurrent_gated_delta_rule_f64(q[:, :, hs], k[:, :, hs], v[:, :, hs], x["g0"][:, :, hs],
+                                                    x["beta0"][:, :, hs], chunk_size=s.block)
+    fo, fs = torch.from_numpy(fo), torch.from_numpy(fs)
+    res["o0_vs_f64"] = _err_stats(g0[:, :, hs], fo, out_b)
+    res["states_vs_f64"] = _err_stats(gs[:, :, hs], fs, st_b)
+    res["oracle_o0_vs_f64_max"] = (o0[:, :, hs].float() - fo.float()).abs().max().item()
+    return res
 
 
 def main(argv=None):
@@ -133,16 +178,20 @@ def _host_info():
 
     import torch
 
-    model = platform.processor() or ""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break  # the first processor's block
+                k, _, v = line.partition(":")
+                fields[k.strip()] = v.strip()
     except OSError:
         pass
-    return {"cpu_model": model, "torch": torch.__version__}
+    model = fields.get("model name") or platform.processor() or ""
+    ident = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return {"cpu_model": f"{model} ({ident})" if ident else model, "cpu_mhz": fields.get("cpu MHz"),
+            "host_logical_cpus": os.cpu_count(), "torch": torch.__version__}
 
 
 GDN_WORKLOADS = {
@@ -183,16 +232,18 @@ def bench_gdn_layer(a):
 
     # timed region: K steps of the schedule between HIP events on the launch stream (the side
     # stream's conv ranges join it through events before its last fork range)
-    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # (an event between consecutive steps gives each step's time as well)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps + 1)]
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
-    s0.record(stream)
-    for _ in range(a.steps):
+    marks[0].record(stream)
+    for i in range(a.steps):
         step()
-    s1.record(stream)
+        marks[i + 1].record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
-    step_ms = s0.elapsed_time(s1) / a.steps
+    step_ms = marks[0].elapsed_time(marks[-1]) / a.steps
+    per_step = [m0.elapsed_time(m1) for m0, m1 in zip(marks, marks[1:])]
 
     # kernels alone: the same K steps as conv, then fork, with HIP events around each kernel
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
@@ -239,7 +290,9 @@ def bench_gdn_layer(a):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(traffic_file),
                      "kernel": "gdn_fork_pipe_kernel", "algorithmic_bytes": core_bytes},
-        "kernels_ms": {"conv_fork": conv_avg, "gdn_state_fork": core_avg},
+        "step_ms": _dist(per_step),
+        "kernels_ms": {"conv_fork": conv_avg, "gdn_state_fork": core_avg,
+                       "conv_fork_dist": _dist(conv_ms), "gdn_state_fork_dist": _dist(core_ms)},
         "schedule": {"pieces": pieces, "ms_per_step_conv_then_fork": seq_step_ms},
         "layer_hbm": {"algorithmic_bytes": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block),
                       "step_gbs": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block) / (step_ms * 1e-3) / 1e9},
@@ -251,10 +304,16 @@ def bench_gdn_layer(a):
     }
     _calibration_copy(a, dev)
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(s, min(a.cpu_sample_L, s.L), a.cpu_budget_s)
+        res["cpu_baseline"], sample = cpu_baseline(s, min(a.cpu_sample_L, s.L), a.cpu_budget_s)
         res["speedup_vs_cpu"] = res["value"] / res["cpu_baseline"]["value"]
+        res["parity"] = parity_sample(plan, s, sample)
     print(json.dumps(res))
     return 0
+
+
+def _dist(ms):
+    """Median, min and max of per-step (or per-launch) times in ms."""
+    return {"median": statistics.median(ms), "min": min(ms), "max": max(ms), "n": len(ms)}
 
 
 def _timed(fn, steps, warmup, stream):

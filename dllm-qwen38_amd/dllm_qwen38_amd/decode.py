@@ -100,6 +100,9 @@ def generate(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int, block
             known[kb * block:][commit] = pick[commit]
             masked[kb * block:][commit] = False
         trace.steps_per_block.append(steps)
+        # the block's host synchronisation: a kernel whose bounded wait gave up chose these tokens
+        # from invalid logits
+        gdn.check_kernel_status("decode block")
         new = known[n:].tolist()
         cur.extend(new)
         trace.generated += len(new)
@@ -386,6 +389,7 @@ def generate_cached(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int
             known[commit] = pick[commit]
             masked[commit] = False
         trace.steps_per_block.append(steps)
+        gdn.check_kernel_status("decode block")
         new = known[have:].tolist()
         cur.extend(new)
         trace.generated += len(new)

@@ -28,6 +28,7 @@ import time
 
 import torch
 
+from . import gdn
 from .blockdiff import BreakMode, block_diffusion_forward, reference_block_logits, reference_clean_logits, tiny_text_model
 
 FAULTS = ("concat-causal-gdn", "mask-leak", "no-conv-prefix")
@@ -56,8 +57,11 @@ def run(cand_model, cand_head, oracle_model, oracle_head, *, block: int, nblocks
 
     def cand(a, b, fault=None):
         with torch.no_grad():
-            return block_diffusion_forward(cand_model, cand_head, a.to(device), b.to(device), block,
-                                           fault=fault, layers=layers)
+            out = block_diffusion_forward(cand_model, cand_head, a.to(device), b.to(device), block,
+                                          fault=fault, layers=layers)
+        # a kernel whose bounded wait gave up wrote invalid logits: stop rather than compare them
+        gdn.check_kernel_status("equivalence harness forward")
+        return out
 
     checks: list[dict] = []
     t0 = time.time()
@@ -105,17 +109,47 @@ def run(cand_model, cand_head, oracle_model, oracle_head, *, block: int, nblocks
     }
 
 
-def _load(model_id: str | None, seed: int):
+def _load(model_id: str | None, seed: int, layers: int | None = None):
+    """(text_model, lm_head, vocab) in fp32 on the CPU. model_id None: the tiny random test model
+    (vocab None). Otherwise a checkpoint directory on disk (no download). With `layers`, the stack
+    is cut to its first `layers` layers BEFORE the fp32 cast: the checkpoint loads in its stored
+    dtype (bf16 for the released weights, so a 27B-class stack fits), the tail layers are dropped,
+    and only the kept prefix is cast. `vocab` reports the embedding rows against the tokenizer's
+    length (the spare rows any id above the tokenizer's range would hit); the tokenizer length is
+    None when the directory holds no tokenizer."""
     if model_id is None:
-        return tiny_text_model(seed=seed)
+        model, head = tiny_text_model(seed=seed)
+        return model, head, None
     from transformers import AutoConfig, AutoModelForCausalLM, AutoModelForImageTextToText
 
-    cfg = AutoConfig.from_pretrained(model_id)
+    cfg = AutoConfig.from_pretrained(model_id, local_files_only=True)
+    kw = dict(dtype="auto" if layers else torch.float32, attn_implementation="eager", local_files_only=True)
     if getattr(cfg, "text_config", None) is not None:
-        m = AutoModelForImageTextToText.from_pretrained(model_id, dtype=torch.float32, attn_implementation="eager")
-        return m.model.language_model.eval(), m.lm_head
-    m = AutoModelForCausalLM.from_pretrained(model_id, dtype=torch.float32, attn_implementation="eager")
-    return m.model.eval(), m.lm_head
+        m = AutoModelForImageTextToText.from_pretrained(model_id, **kw)
+        text_model, head = m.model.language_model, m.lm_head
+        if hasattr(m.model, "visual"):
+            m.model.visual = None  # the vision tower is never run
+    else:
+        m = AutoModelForCausalLM.from_pretrained(model_id, **kw)
+        text_model, head = m.model, m.lm_head
+    if layers:
+        if layers > len(text_model.layers):
+            raise ValueError(f"--layers {layers} exceeds the model's {len(text_model.layers)} layers")
+        del text_model.layers[layers:]
+        text_model.config.num_hidden_layers = layers
+        text_model.config.layer_types = list(text_model.config.layer_types[:layers])
+    text_model.float().eval()
+    head.float()
+    rows = int(text_model.embed_tokens.weight.shape[0])
+    try:
+        from transformers import AutoTokenizer
+
+        tok_len = len(AutoTokenizer.from_pretrained(model_id, local_files_only=True))
+    except Exception:  # noqa: BLE001 - a checkpoint without tokenizer files still runs
+        tok_len = None
+    vocab = {"embedding_rows": rows, "tokenizer_len": tok_len,
+             "spare_rows": None if tok_len is None else rows - tok_len}
+    return text_model, head, vocab
 
 
 def main(argv: list[str] | None = None) -> int:
@@ -144,7 +178,7 @@ def main(argv: list[str] | None = None) -> int:
         print("COULD-NOT-MEASURE nblocks < 1", file=sys.stderr)
         return 2
     try:
-        oracle_model, oracle_head = _load(a.model, a.seed)
+        oracle_model, oracle_head, vocab = _load(a.model, a.seed, a.layers)
     except Exception as e:  # noqa: BLE001 - could not measure is its own exit code
         print(f"COULD-NOT-MEASURE model load failed: {type(e).__name__}: {e}", file=sys.stderr)
         return 2
@@ -168,6 +202,8 @@ def main(argv: list[str] | None = None) -> int:
     rep["model"] = a.model or "tiny-random"
     rep["attn"] = a.attn
     rep["oracle_gdn_kernel"] = oracle_gdn_kernel()
+    if vocab is not None:
+        rep["vocab"] = vocab
     if a.json:
         with open(a.json, "w") as f:
             json.dump(rep, f, indent=1)
@@ -179,6 +215,9 @@ def main(argv: list[str] | None = None) -> int:
     print(f"CHECKS\t{rep['checks_passed']}/{rep['checks_total']}\tFAULTS-DETECTED\t{rep['faults_detected']}/"
           f"{rep['faults_total']}\tmodel={rep['model']} layers={rep['layers']} L={rep['seq_len']} dtype={rep['dtype']} "
           f"oracle-gdn={rep['oracle_gdn_kernel']} {rep['seconds']}s")
+    if vocab is not None:
+        print(f"VOCAB\tembedding_rows={vocab['embedding_rows']}\ttokenizer_len={vocab['tokenizer_len']}\t"
+              f"spare_rows={vocab['spare_rows']}")
     ok = rep["checks_passed"] == rep["checks_total"] and rep["faults_detected"] == rep["faults_total"]
     return 0 if ok else 1
 

@@ -115,15 +115,16 @@ def _core(q, k, v, g, beta, *, chunk_size, initial_state, need_states):
 
 
 def causal_conv1d_fn(hidden_states: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
-                     activation: str | None = None, seq_idx=None, initial_states: torch.Tensor | None = None,
-                     return_final_states: bool = False, final_states_out: torch.Tensor | None = None, *,
+                     activation: str | None = None, *, seq_idx=None, initial_states: torch.Tensor | None = None,
+                     return_final_states: bool = False, final_states_out: torch.Tensor | None = None,
                      conv_prefix: torch.Tensor | None = None):
     """Causal depthwise conv [B, C, T] -> [B, C, T] (transformers modeling_qwen3_5.py:219-239), with
     an optional [B, C, P] prefix: equal to the conv over cat([prefix, x]) cut to the last T outputs
     (reference gdn.py:217-219). The result is a [B, C, T] view of token-major [B, T, C] storage.
 
-    The keyword arguments of the causal-conv1d package's function that the seam may pass are
-    honoured or refused, never dropped: `initial_states` [B, C, K-1] is the prefix under that
+    The positional parameters are those of the transformers fallback (x, weight, bias, activation).
+    The causal-conv1d package's other arguments, which the seam passes by keyword, are
+    keyword-only here and are honoured or refused, never dropped: `initial_states` [B, C, K-1] is the prefix under that
     package's name; `return_final_states` also returns the last K-1 inputs of the extended sequence
     ([B, C, K-1], written into `final_states_out` when given); `seq_idx` (packed sequences) is
     not supported and raises."""
@@ -396,6 +397,16 @@ def _launch_ranges(Lb, dev, cuts, conv, fork, dims):
     for t in (r0, rt, w, bias, y0, yt, tails):
         if t is not None:
             t.record_stream(side)
+
+
+def check_kernel_status(where: str) -> None:
+    """Raise RuntimeError when a bounded wait inside a kernel gave up since the last check (the
+    outputs of the launches since then are invalid); resets the bits. Synchronises the device, so
+    callers place it where they synchronise anyway."""
+    st = kernel_status(reset=True)
+    if st:
+        raise RuntimeError(f"{where}: a bounded wait inside a HIP kernel gave up (status bits {st:#x}); the outputs "
+                           "of the launches since the last status check are invalid")
 
 
 def kernel_status(reset: bool = True) -> int:

@@ -3,18 +3,21 @@
 import torch
 
 
-def tiny_hf_model(seed=0, layers=8, vocab=256, norm_std=0.1):
+def tiny_hf_model(seed=0, layers=8, vocab=256, norm_std=0.1, linear_heads=(2, 4), linear_head_dim=16):
     """transformers' own Qwen3_5TextModel at hidden 64 (6 GDN + 2 attention layers, attention heads
     4/2 of dim 16, GDN heads 2 key / 4 value of dim 16, conv width 4), fp32 on the CPU, plus an
-    untied lm_head. Norm weights are drawn N(0, norm_std) so every weight path is exercised."""
+    untied lm_head. Norm weights are drawn N(0, norm_std) so every weight path is exercised.
+    `linear_heads` (key, value) and `linear_head_dim` change the GDN heads (128-wide heads in bf16
+    run the pipelined fork kernel)."""
     from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
     from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextModel
 
     torch.manual_seed(seed)
     cfg = Qwen3_5TextConfig(
         vocab_size=vocab, hidden_size=64, intermediate_size=128, num_hidden_layers=layers,
-        num_attention_heads=4, num_key_value_heads=2, head_dim=16, linear_num_key_heads=2,
-        linear_num_value_heads=4, linear_key_head_dim=16, linear_value_head_dim=16, linear_conv_kernel_dim=4,
+        num_attention_heads=4, num_key_value_heads=2, head_dim=16, linear_num_key_heads=linear_heads[0],
+        linear_num_value_heads=linear_heads[1], linear_key_head_dim=linear_head_dim,
+        linear_value_head_dim=linear_head_dim, linear_conv_kernel_dim=4,
         max_position_embeddings=4096,
         rope_parameters={"rope_theta": 10000.0, "mrope_section": [2, 1, 1], "partial_rotary_factor": 0.25},
         attn_implementation="eager")

@@ -22,3 +22,20 @@ def dev():
     if not torch.cuda.is_available():
         pytest.fail("GPU test selected but no ROCm device is visible")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _kernel_status_clean(request):
+    """After every GPU test: no bounded wait inside a kernel gave up (a set status bit means some
+    launch of the test produced invalid outputs, whatever the test compared)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    import torch
+
+    if not torch.cuda.is_available():
+        return
+    from dllm_qwen38_amd import gdn
+
+    st = gdn.kernel_status(reset=True)
+    assert st == 0, f"a bounded wait inside a HIP kernel gave up during this test (status bits {st:#x})"

@@ -7,8 +7,16 @@ contracts are among them: `T % chunk` (src/dllm_qwen38/gdn.py:70-71) and `L % bl
 import ctypes
 
 import pytest
+import torch
 
 from dllm_qwen38_amd import _lib
+
+# The placeholder addresses must never reach a device: should a host-side check regress, the call
+# would launch a kernel on an unmapped address. These checks need no GPU, so where a ROCm device is
+# visible (a full, unfiltered run on a GPU machine) the module is skipped; the CPU suite runs them.
+if torch.cuda.device_count() > 0:
+    pytest.skip("host-only refusal checks with placeholder device addresses: skipped where a GPU is visible",
+                allow_module_level=True)
 
 EINVAL, EUNSUP = -1, -2
 P = 1 << 16            # a 16-byte aligned placeholder address

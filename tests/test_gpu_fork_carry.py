@@ -150,3 +150,44 @@ def test_chunk_kernel_bf16_matches_oracle(dev, B, Hk, Hv, chunk):
     _check(f"chunk {chunk} {B}x{Hv} out", out.cpu(), ro, out_bound)
     _check(f"chunk {chunk} {B}x{Hv} states", st.cpu(), rs, state_bound)
 
+
+
+@pytest.mark.parametrize("chunk", [8, 4, 2, 1])
+def test_chunk_rule_bf16_short_chunks_on_the_pipelined_kernel(dev, chunk):
+    """Chunks shorter than 8 rows per 32-row tile (every chunk that divides 32 runs the pipelined
+    kernel on one stream; the tile then holds `chunk` real rows and zero padding), with an initial
+    state and slow decay, against the oracle and the float64 token recurrence."""
+    B, Hk, Hv, T = 1, 2, 8, 64
+    q, k, v, g, beta = inputs.gdn_core_inputs(B, T, Hk, Hv, 128, torch.bfloat16, seed=7350 + chunk, g_shift=SLOW)
+    init = torch.randn(B, Hv, 128, 128, generator=torch.Generator().manual_seed(7360 + chunk)) * 0.5
+    out, st = gdn.chunk_gated_delta_rule_with_states(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), chunk,
+                                                     initial_state=init.to(dev))
+    torch.cuda.synchronize()
+    qe, ke = q.repeat_interleave(Hv // Hk, 2), k.repeat_interleave(Hv // Hk, 2)
+    ro, rs = gdn_ref.chunk_gated_delta_rule_with_states(qe, ke, v, g, beta, chunk, initial_state=init)
+    assert st.shape == (B, T // chunk, Hv, 128, 128)
+    _check(f"chunk {chunk} out", out.cpu(), ro, out_bound)
+    _check(f"chunk {chunk} states", st.cpu(), rs, state_bound)
+    fo, fs = gdn_ref.recurrent_gated_delta_rule_f64(qe, ke, v, g, beta, chunk_size=chunk, initial_state=init)
+    _check(f"chunk {chunk} out vs f64", out.cpu(), torch.from_numpy(fo), out_bound)
+    _check(f"chunk {chunk} states vs f64", st.cpu(), torch.from_numpy(fs), state_bound)
+
+
+@pytest.mark.parametrize("chunk", [32, 16, 64])
+def test_chunk_rule_bf16_without_qk_l2norm(dev, chunk):
+    """use_qk_l2norm_in_kernel=False: q and k enter unnormalised (the kernels' no-norm branches: unit
+    k-row scales and q scaled by Dk^-1/2 alone). Inputs are drawn with rows of norm about 1, as the
+    recurrence needs bounded keys, on both kernels (chunks 32 / 16 pipelined, 64 the chunk kernel)."""
+    B, Hk, Hv, T = 2, 2, 8, 256
+    q, k, v, g, beta = inputs.gdn_core_inputs(B, T, Hk, Hv, 128, torch.bfloat16, seed=7450 + chunk, g_shift=SLOW)
+    q = (q.float() / 128 ** 0.5).to(torch.bfloat16)
+    k = (k.float() / 128 ** 0.5).to(torch.bfloat16)
+    out, st = gdn.chunk_gated_delta_rule_with_states(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), chunk,
+                                                     use_qk_l2norm_in_kernel=False)
+    torch.cuda.synchronize()
+    qe, ke = q.repeat_interleave(Hv // Hk, 2), k.repeat_interleave(Hv // Hk, 2)
+    ro, rs = gdn_ref.chunk_gated_delta_rule_with_states(qe, ke, v, g, beta, chunk, use_qk_l2norm_in_kernel=False)
+    _check(f"no l2norm chunk {chunk} out", out.cpu(), ro, out_bound)
+    _check(f"no l2norm chunk {chunk} states", st.cpu(), rs, state_bound)
+    fo, fs = gdn_ref.recurrent_gated_delta_rule_f64(qe, ke, v, g, beta, chunk_size=chunk, use_qk_l2norm=False)
+    _check(f"no l2norm chunk {chunk} out vs f64", out.cpu(), torch.from_numpy(fo), out_bound)

@@ -203,7 +203,11 @@ def gdn_mixer_forward(
     q, k, v = _split_qkv(mixed, m, B, T)
     core, states = _core(q, k, v, g, beta, chunk_size=chunk_size, initial_state=initial_state,
                          need_states=need_states)
-    core = m.norm(core.reshape(-1, m.head_v_dim), z.reshape(-1, m.head_v_dim)).reshape(B, T, -1)
+    # the module's gated RMSNorm (Qwen3_5RMSNormGated: rmsnorm(core) * w * silu(z), [hf]:168-184) on
+    # the HIP kernel, with the module's weight and epsilon
+    Dv = m.head_v_dim
+    eps = float(getattr(m.norm, "variance_epsilon", getattr(m.norm, "eps", 1e-6)))
+    core = norms.gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm.weight, eps).reshape(B, T, -1)
     return m.out_proj(core), states, raw.transpose(1, 2)
 
 

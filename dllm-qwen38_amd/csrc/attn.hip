@@ -47,6 +47,20 @@ struct AttnArgs {
   float* mlpart;      // ksplit > 1: running max and sum [ksplit][B][M][Hq][2] fp32
   float scale_log2e;  // softmax scale * log2(e)
   int vec;            // 16-byte vector loads of q/k/v rows allowed
+  // gated attention layer, fused (direct-load kernel, complementary-mask mode only):
+  // q_norm_w non-null: q is the raw q_proj output; each query row is RMSNorm(1 + w)-normalised and
+  // its first `rd` dims rotated (rotate_half, position = row index within its half) as it is
+  // loaded, with the rounding of the separate q/k norm + RoPE kernel
+  const void* q_norm_w;
+  int q_norm_f32;  // the weight is fp32 (else bf16)
+  float q_eps;
+  const void* cosb;  // [L, rd] rotary tables in the activation dtype
+  const void* sinb;
+  int rd;
+  // gate non-null: out = attention * sigmoid(gate), gate [B, 2L, Hq, d] with these strides
+  const void* gate;
+  long long g_sb;
+  int g_st, g_sh;
 };
 
 // Work unit of dispatch slot bid among n. The dispatcher hands slot bid to XCD bid % 8, in order of
@@ -435,6 +449,85 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// RMSNorm(1 + w) and rotate_half RoPE of one query row held as the direct-load kernel's Q^T
+// fragments (lane (row, h): slice s holds d = 32 s + 8 h + (0..7) in lo and 32 s + 16 + 8 h +
+// (0..7) in hi, the other half of the row in lane ^ 32). The rounding follows the separate q/k
+// norm + RoPE kernel (qk_norm_rope256_kernel): n = bf16((x / rms) (1 + w)), and in the first rd
+// dims bf16(bf16(n cos) + bf16(+-partner sin)). The rotation pairs d with d + rd / 2, which with
+// rd / 2 a multiple of 32 is the same position of slice s + rd / 64: in the same lane.
+// rotate_half over slice pairs (s, s + NH), s < NH: d pairs with d + 32 NH (rotary_dim = 64 NH)
+template <int D, int NH>
+__device__ __forceinline__ void rope_pairs(Frag<true> (&qf)[D / 32], const bf16* cs, const bf16* sn, int h) {
+#pragma unroll
+  for (int s = 0; s < NH; ++s)
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+      const int d1 = 32 * s + 16 * part + 8 * h, d2 = d1 + 32 * NH;
+      const bf16x8 c1 = *(const bf16x8*)(cs + d1), s1 = *(const bf16x8*)(sn + d1);
+      const bf16x8 c2 = *(const bf16x8*)(cs + d2), s2 = *(const bf16x8*)(sn + d2);
+      bf16x8& x1 = part ? qf[s].hi : qf[s].lo;
+      bf16x8& x2 = part ? qf[s + NH].hi : qf[s + NH].lo;
+      __builtin_amdgcn_sched_barrier(0);  // one pair of runs at a time (register pressure)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float a1 = (float)x1[i], a2 = (float)x2[i];
+        const float o1 = (float)(bf16)((float)(bf16)(a1 * (float)c1[i]) + (float)(bf16)(-a2 * (float)s1[i]));
+        const float o2 = (float)(bf16)((float)(bf16)(a2 * (float)c2[i]) + (float)(bf16)(a1 * (float)s2[i]));
+        x1[i] = (bf16)o1;
+        x2[i] = (bf16)o2;
+      }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void q_norm_rope(Frag<true> (&qf)[D / 32], const AttnArgs& a, int pos, int h) {
+  constexpr int DT = D / 32;
+  // sum of squares from the bf16 pairs (paired dot products: no unpacked copy of the row is held)
+  float ss = 0.f;
+#pragma unroll
+  for (int s = 0; s < DT; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bf16x2 lo = {qf[s].lo[2 * i], qf[s].lo[2 * i + 1]};
+      const bf16x2 hi = {qf[s].hi[2 * i], qf[s].hi[2 * i + 1]};
+      ss = __builtin_amdgcn_fdot2_f32_bf16(lo, lo, ss, false);
+      ss = __builtin_amdgcn_fdot2_f32_bf16(hi, hi, ss, false);
+    }
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+  const float inv = rsqrtf((__uint_as_float(r[0]) + __uint_as_float(r[1])) / (float)D + a.q_eps);
+#pragma unroll
+  for (int s = 0; s < DT; ++s)
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+      __builtin_amdgcn_sched_barrier(0);  // one 8-element run at a time (register pressure)
+      const int d0 = 32 * s + 16 * part + 8 * h;
+      float w[8];
+      if (a.q_norm_f32) {
+        const f32x4 w0 = *(const f32x4*)((const float*)a.q_norm_w + d0);
+        const f32x4 w1 = *(const f32x4*)((const float*)a.q_norm_w + d0 + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = w0[i], w[4 + i] = w1[i];
+      } else {
+        const bf16x8 w8 = *(const bf16x8*)((const bf16*)a.q_norm_w + d0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = (float)w8[i];
+      }
+      bf16x8& q8 = part ? qf[s].hi : qf[s].lo;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q8[i] = (bf16)((float)q8[i] * inv * (1.f + w[i]));
+    }
+  const bf16* const cs = (const bf16*)a.cosb + (long long)pos * a.rd;
+  const bf16* const sn = (const bf16*)a.sinb + (long long)pos * a.rd;
+  // rotated slice pairs (s, s + rd / 64), with compile-time slice indices (registers, not scratch)
+  switch (a.rd / 64) {
+    case 1: rope_pairs<D, 1>(qf, cs, sn, h); break;
+    case 2: if constexpr (D / 32 >= 4) rope_pairs<D, 2>(qf, cs, sn, h); break;
+    case 3: if constexpr (D / 32 >= 6) rope_pairs<D, 3>(qf, cs, sn, h); break;
+    case 4: if constexpr (D / 32 >= 8) rope_pairs<D, 4>(qf, cs, sn, h); break;
+    default: break;
+  }
+}
+
 template <int D>
 struct SpSmem {
   // K and V ring stages: four at d = 256 (one phase more of loads in flight, measured 4% faster),
@@ -580,6 +673,9 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
       for (int s = 0; s < DT; ++s) {
         qf[s].lo = *(const bf16x8*)(qp + 32 * s + 8 * h);
         qf[s].hi = *(const bf16x8*)(qp + 32 * s + 16 + 8 * h);
+      }
+      if constexpr (!BC) {
+        if (a.q_norm_w) q_norm_rope<D>(qf, a, row, h);  // the row's position within its half
       }
     }
     // keys visible to this lane's query in each half: [vlo, vhi) (empty past the last query)
@@ -781,15 +877,32 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
     const float inv = 1.f / lfin;
     const long long orow = BC ? (long long)b * Lq + qi : (long long)b * 2 * L + qh * L + qi;
     bf16* op = (bf16*)a.out + (orow * a.Hq + hq) * a.d;
+    // the output gate (gated attention, [hf]:698): bf16(bf16(o) * bf16(sigmoid(gate))), the
+    // rounding of the separate elementwise product
+    const bf16* gp = nullptr;
+    if constexpr (!BC)
+      if (a.gate) gp = (const bf16*)a.gate + b * a.g_sb + (long long)(qh * L + qi) * a.g_st + (long long)hq * a.g_sh;
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+    for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         bf16x4 o4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o4[i] = (bf16)(O[t][4 * m + i] * inv);
+        if (gp) {
+          const bf16x4 g4 = *(const bf16x4*)(gp + 32 * t + 8 * m + 4 * h);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float sg = (float)(bf16)(1.f / (1.f + expf(-(float)g4[i])));
+            o4[i] = (bf16)((float)o4[i] * sg);
+          }
+        }
         *(bf16x4*)(op + 32 * t + 8 * m + 4 * h) = o4;
       }
+      // one d slice at a time: the gate loads of later slices are not hoisted above this one's
+      // stores (they would hold registers beside the whole accumulator)
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -918,6 +1031,76 @@ extern "C" int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, co
   a.leak = flags & 1;
   a.scale_log2e = scale * 1.4426950408889634f;
   return dispatch_attn<false>(a, sts, dtype, (hipStream_t)stream);
+}
+
+extern "C" int dllm_bd_attention_gated_supported(int d, int rotary_dim, int dtype) {
+  return dtype == DT_BF16 && (d == 64 || d == 128 || d == 256) && rotary_dim >= 0 && rotary_dim % 64 == 0 &&
+         rotary_dim <= d;
+}
+
+extern "C" int dllm_bd_attention_gated_fwd(const void* q, const int64_t* q_strides, const void* k,
+                                           const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                           const void* gate, const int64_t* gate_strides, const void* q_norm_w,
+                                           int q_norm_dtype, float q_norm_eps, const void* cos_table,
+                                           const void* sin_table, int rotary_dim, void* out, int B, int L, int Hq,
+                                           int Hkv, int d, int block, float scale, int dtype, int flags, void* stream) {
+  if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides)
+    return fail(DLLM_EINVAL, "gated attention: null pointer");
+  if (gate && !gate_strides) return fail(DLLM_EINVAL, "gated attention: gate without strides");
+  if (q_norm_w && rotary_dim > 0 && (!cos_table || !sin_table))
+    return fail(DLLM_EINVAL, "gated attention: null rotary table");
+  if (B <= 0 || L <= 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || block <= 0)
+    return fail(DLLM_EINVAL, "gated attention: bad sizes B=%d L=%d Hq=%d Hkv=%d d=%d block=%d", B, L, Hq, Hkv, d, block);
+  if (L % block) return fail(DLLM_EINVAL, "L=%d is not a multiple of block=%d", L, block);
+  if (Hq % Hkv) return fail(DLLM_EINVAL, "attention: Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+  if (!dllm_bd_attention_gated_supported(d, q_norm_w ? rotary_dim : 0, dtype))
+    return fail(DLLM_EUNSUPPORTED, "gated attention: fused form needs bf16, d in {64, 128, 256} and a rotary_dim "
+                "that is a multiple of 64 (d=%d rotary_dim=%d dtype=%d)", d, rotary_dim, dtype);
+  if (q_norm_w && q_norm_dtype != DT_BF16 && q_norm_dtype != DT_F32)
+    return fail(DLLM_EUNSUPPORTED, "gated attention: q norm weight dtype %d", q_norm_dtype);
+  const int64_t* const sts[3] = {q_strides, k_strides, v_strides};
+  const int H[3] = {Hq, Hkv, Hkv};
+  for (int i = 0; i < 3; ++i)
+    if (!fits32(2LL * L * sts[i][1]) || !fits32((long long)H[i] * sts[i][2]) ||
+        !fits32(2LL * L * sts[i][1] + (long long)H[i] * sts[i][2]))
+      return fail(DLLM_EUNSUPPORTED, "attention: per-sequence extent exceeds 32-bit element offsets");
+  if (gate && (!fits32(2LL * L * gate_strides[1] + (long long)Hq * gate_strides[2]) || gate_strides[1] % 4 ||
+               gate_strides[2] % 4 || (uintptr_t)gate % 8))
+    return fail(DLLM_EUNSUPPORTED, "gated attention: gate rows must be 8-byte aligned with 32-bit extents");
+  const uintptr_t al = (uintptr_t)q_norm_w | (uintptr_t)cos_table | (uintptr_t)sin_table;
+  if (q_norm_w && (al % 16 || rotary_dim % 8))
+    return fail(DLLM_EUNSUPPORTED, "gated attention: norm weight and rotary tables must be 16-byte aligned");
+  AttnArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.out = out;
+  fill_strides(a, q_strides, k_strides, v_strides);
+  a.B = B; a.L = L; a.Hq = Hq; a.Hkv = Hkv; a.d = d; a.C = block;
+  a.leak = flags & 1;
+  a.scale_log2e = scale * 1.4426950408889634f;
+  a.q_norm_w = q_norm_w;
+  a.q_norm_f32 = q_norm_dtype == DT_F32;
+  a.q_eps = q_norm_eps;
+  a.cosb = cos_table;
+  a.sinb = sin_table;
+  a.rd = rotary_dim;
+  a.gate = gate;
+  if (gate) {
+    a.g_sb = gate_strides[0];
+    a.g_st = (int)gate_strides[1];
+    a.g_sh = (int)gate_strides[2];
+  }
+  // the fused prologue and epilogue live in the direct-load kernel only: refuse a layout it does not take
+  const int esz = 2, vel = 16 / esz;
+  bool vec = true;
+  for (int i = 0; i < 3; ++i) vec = vec && (sts[i][0] % vel == 0) && (sts[i][1] % vel == 0) && (sts[i][2] % vel == 0);
+  vec = vec && ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0);
+  if (!vec || !(a.scale_log2e > 0.f && a.scale_log2e < INFINITY))
+    return fail(DLLM_EUNSUPPORTED, "gated attention: q/k/v rows must be 16-byte aligned and the scale positive");
+  a.vec = 1;
+  switch (d) {
+    case 64: return launch_attn_sp<64, false>(a, (hipStream_t)stream);
+    case 128: return launch_attn_sp<128, false>(a, (hipStream_t)stream);
+    default: return launch_attn_sp<256, false>(a, (hipStream_t)stream);
+  }
 }
 
 extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, const void* k,

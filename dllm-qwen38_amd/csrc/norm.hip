@@ -514,9 +514,12 @@ extern "C" int dllm_qk_norm_rope_fwd(const void* q, const int64_t* q_strides, co
                                      const void* sin_table, void* q_out, void* k_out, int B, int S, int L, int Hq,
                                      int Hkv, int head_dim, int rotary_dim, float eps, int dtype, int dtype_w,
                                      void* stream) {
-  if (!q || !k || !q_strides || !k_strides || !q_norm_w || !k_norm_w || !q_out || !k_out)
+  // Hq == 0: the k rows alone (q, q_strides, q_norm_w and q_out may then be null)
+  if ((Hq > 0 && (!q || !q_strides || !q_norm_w || !q_out)) || !k || !k_strides || !k_norm_w || !k_out)
     return fail(DLLM_EINVAL, "qk norm rope: null pointer");
-  if (B <= 0 || S <= 0 || L <= 0 || Hq <= 0 || Hkv <= 0 || head_dim <= 0 || head_dim > 256 || rotary_dim < 0 ||
+  static const int64_t zero3[3] = {0, 0, 0};
+  if (Hq == 0) q_strides = zero3;
+  if (B <= 0 || S <= 0 || L <= 0 || Hq < 0 || Hkv <= 0 || head_dim <= 0 || head_dim > 256 || rotary_dim < 0 ||
       rotary_dim > head_dim || (rotary_dim & 1))
     return fail(DLLM_EINVAL, "qk norm rope: bad sizes B=%d S=%d L=%d Hq=%d Hkv=%d hd=%d rd=%d", B, S, L, Hq, Hkv,
                 head_dim, rotary_dim);

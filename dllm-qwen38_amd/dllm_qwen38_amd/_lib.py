@@ -68,6 +68,11 @@ _SIGNATURES = {
     "dllm_bd_attention_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p]),
+    "dllm_bd_attention_gated_supported": (_c_int, [_c_int, _c_int, _c_int]),
+    "dllm_bd_attention_gated_fwd": (_c_int, [
+        _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int,
+        _c_float, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+        _c_int, _c_int, _c_void_p]),
     "dllm_decode_linear_workgroups": (_c_int, [_c_int, _c_int, _c_int]),
     "dllm_decode_linear_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int]),
     "dllm_decode_linear_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,

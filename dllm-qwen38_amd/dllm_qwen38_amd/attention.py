@@ -76,6 +76,54 @@ def bd_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: in
     return out
 
 
+def gated_supported(q: torch.Tensor, d: int, rotary_dim: int) -> bool:
+    """Whether bd_attention_gated takes this shape in one launch (bf16, d in {64, 128, 256},
+    rotary_dim a multiple of 64)."""
+    return bool(_lib.lib().dllm_bd_attention_gated_supported(d, rotary_dim, _lib.dtype_code(q.dtype)))
+
+
+def bd_attention_gated(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor | None, *, block: int,
+                       q_norm_weight: torch.Tensor | None = None, q_norm_eps: float = 1e-6,
+                       cos: torch.Tensor | None = None, sin: torch.Tensor | None = None, scale: float | None = None,
+                       leak_xt_prefix: bool = False) -> torch.Tensor:
+    """The gated attention layer's core in one launch ([hf]:672-698 around bd_attention): with
+    q_norm_weight, q [B, 2L, Hq, d] is the raw q_proj query half, RMSNorm(1 + w)-normalised and its
+    first rotary_dim dims rotated (cos/sin [L, rotary_dim], the activation dtype, row = position
+    within the half) as the kernel loads it; k must already be normed and rotated
+    (norms.k_norm_rope). With gate [B, 2L, Hq, d], the output is multiplied by sigmoid(gate), each
+    rounded to the dtype as the separate elementwise ops round. Returns [B, 2L, Hq, d] contiguous.
+    Shapes gated_supported() refuses raise; callers run the separate launches for them."""
+    dev = _lib.require_device(q, k, v, gate, q_norm_weight, cos, sin)
+    B, S, Hq, d = q.shape
+    if S % 2:
+        raise ValueError(f"sequence {S} is not cat([x_t, x_0]) of two equal halves")
+    L = S // 2
+    if L % block:
+        raise ValueError(f"L={L} is not a multiple of block={block}")
+    if k.shape[:2] != (B, S) or v.shape != k.shape or k.shape[-1] != d:
+        raise ValueError("k and v must be [B, 2L, Hkv, d] matching q")
+    Hkv = k.shape[2]
+    if gate is not None and (tuple(gate.shape) != (B, S, Hq, d) or gate.stride(-1) != 1 or gate.dtype != q.dtype):
+        raise ValueError("gate must be [B, 2L, Hq, d] of q's dtype with its last dim contiguous")
+    rd = 0
+    if q_norm_weight is not None:
+        if cos is None or sin is None or cos.shape != sin.shape or cos.shape[0] < L:
+            raise ValueError("the q prologue needs cos/sin tables [L, rotary_dim]")
+        rd = int(cos.shape[-1])
+        cos, sin = cos.to(q.dtype).contiguous(), sin.to(q.dtype).contiguous()
+        q_norm_weight = q_norm_weight.contiguous()
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    out = torch.empty(B, S, Hq, d, dtype=q.dtype, device=dev)
+    sc = d ** -0.5 if scale is None else float(scale)
+    _lib.check(_lib.lib().dllm_bd_attention_gated_fwd(
+        q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
+        _lib.ptr(gate), None if gate is None else _lib.strides3(gate), _lib.ptr(q_norm_weight),
+        _lib.dtype_code(q_norm_weight.dtype) if q_norm_weight is not None else 0, float(q_norm_eps),
+        _lib.ptr(cos), _lib.ptr(sin), rd, out.data_ptr(), B, L, Hq, Hkv, d, block, sc, _lib.dtype_code(q.dtype),
+        1 if leak_xt_prefix else 0, _lib.stream_handle(dev)), "dllm_bd_attention_gated_fwd")
+    return out
+
+
 def _key_splits(q: torch.Tensor, M: int, N: int, d: int) -> int:
     """Key splits for a decoding step (bf16, the direct-load kernel's head sizes, few query rows):
     about eight 32-key tiles per workgroup; 1 otherwise."""

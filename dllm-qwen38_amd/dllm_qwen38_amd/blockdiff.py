@@ -131,12 +131,23 @@ def _attention_arm(att, n: torch.Tensor, cos, sin, block: int, fault: BreakMode)
     S = 2 * L
     hd = att.head_dim
     q, gate = torch.chunk(att.q_proj(x).view(B, S, -1, 2 * hd), 2, dim=-1)
-    gate = gate.reshape(B, S, -1)
-    q, k = norms.qk_norm_rope(q, att.k_proj(x).view(B, S, -1, hd), att.q_norm, att.k_norm, cos, sin, L)
     v = att.v_proj(x).view(B, S, -1, hd)
-    o = attention.bd_attention(q, k, v, block=block, scale=float(att.scaling), leak_xt_prefix=fault.leak_xt_prefix)
-    out = att.o_proj(o.reshape(B, S, -1) * torch.sigmoid(gate))
+    if attention.gated_supported(q, hd, cos.shape[-1]) and _aligned16(q, v, att.q_norm.weight, cos, sin):
+        # one launch: q norm + RoPE as the kernel loads q, the sigmoid gate as it stores the output
+        k = norms.k_norm_rope(att.k_proj(x).view(B, S, -1, hd), att.k_norm, cos, sin, L)
+        o = attention.bd_attention_gated(q, k, v, gate, block=block, q_norm_weight=att.q_norm.weight,
+                                         q_norm_eps=_eps(att.q_norm), cos=cos, sin=sin, scale=float(att.scaling),
+                                         leak_xt_prefix=fault.leak_xt_prefix)
+        out = att.o_proj(o.reshape(B, S, -1))
+    else:
+        q, k = norms.qk_norm_rope(q, att.k_proj(x).view(B, S, -1, hd), att.q_norm, att.k_norm, cos, sin, L)
+        o = attention.bd_attention(q, k, v, block=block, scale=float(att.scaling), leak_xt_prefix=fault.leak_xt_prefix)
+        out = att.o_proj(o.reshape(B, S, -1) * torch.sigmoid(gate.reshape(B, S, -1)))
     return out.view(B, 2, L, -1).transpose(0, 1).reshape(2 * B, L, -1)
+
+
+def _aligned16(*ts) -> bool:
+    return all(t.data_ptr() % 16 == 0 for t in ts)
 
 
 def layer_step_stacked(layer, kind: str, h: torch.Tensor, *, block: int, cos, sin, fault: BreakMode | None = None,

@@ -107,6 +107,24 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_norm, k_norm, cos: torch.Te
     return qo, ko
 
 
+def k_norm_rope(k: torch.Tensor, k_norm, cos: torch.Tensor, sin: torch.Tensor, L: int) -> torch.Tensor:
+    """The k half of qk_norm_rope alone (its q prologue runs inside the attention kernel):
+    k [B, S, Hkv, hd] -> contiguous normed-and-rotated copy."""
+    dev = _lib.require_device(k, cos, sin)
+    B, S, Hkv, hd = k.shape
+    if k.stride(-1) != 1:
+        raise ValueError("k last dim must be contiguous")
+    rd = cos.shape[-1]
+    cs, sn = _c(cos.to(k.dtype)), _c(sin.to(k.dtype))
+    wk = _c(k_norm.weight)
+    ko = torch.empty(B, S, Hkv, hd, dtype=k.dtype, device=dev)
+    _lib.check(_lib.lib().dllm_qk_norm_rope_fwd(
+        None, None, k.data_ptr(), _lib.strides3(k), None, wk.data_ptr(), cs.data_ptr(), sn.data_ptr(), None,
+        ko.data_ptr(), B, S, L, 0, Hkv, hd, rd, _eps(k_norm), _lib.dtype_code(k.dtype), _lib.dtype_code(wk.dtype),
+        _lib.stream_handle(dev)), "dllm_qk_norm_rope_fwd")
+    return ko
+
+
 def gdn_gates(b: torch.Tensor, a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor):
     """Gated DeltaNet gates (reference gdn.py:225-226) in one kernel: beta = sigmoid(b) rounded to
     b's dtype and returned in fp32 (the core takes fp32 beta), g = -exp(A_log) * softplus(a + dt_bias)

@@ -182,6 +182,29 @@ int dllm_bd_attention_fwd(const void* q, const int64_t* q_strides, const void* k
                           int d, int block, float scale, int dtype, int flags, void* stream);
 
 /*
+ * The gated attention layer's core in one launch: dllm_bd_attention_fwd with the q prologue and the
+ * output gate fused in. Replaces, of Qwen3_5Attention.forward ([hf]:656-701, called from
+ * src/dllm_qwen38/blockdiff.py:178-182), the q RMSNorm(1 + w) ([hf]:672), the partial RoPE of q
+ * ([hf]:676, apply_rotary_pos_emb [hf]:554-589), the attention ([hf]:682-695) and the sigmoid
+ * output gate ([hf]:698); k arrives already normed and rotated (dllm_qk_norm_rope_fwd with Hq = 0),
+ * v as projected. q_norm_w non-null: q [B,2L,Hq,d] is the raw q_proj query half (any strides, last
+ * dim contiguous); each row is normalised with q_norm_w (q_norm_dtype 0 fp32 / 1 bf16) and q_norm_eps
+ * and its first rotary_dim dims rotated with the [L, rotary_dim] cos/sin tables (activation dtype)
+ * at the row's position within its half, rounded as dllm_qk_norm_rope_fwd rounds. q_norm_w null: q
+ * is used as given. gate non-null: out = bf16(bf16(attention) * bf16(sigmoid(gate))) with gate
+ * [B,2L,Hq,d] at gate_strides (the q_proj gate half). bf16, d in {64, 128, 256}, rotary_dim a
+ * multiple of 64 (dllm_bd_attention_gated_supported), 16-byte aligned q/k/v rows, norm weight and
+ * tables; anything else returns -2 (the caller runs the separate launches).
+ */
+int dllm_bd_attention_gated_supported(int d, int rotary_dim, int dtype);
+int dllm_bd_attention_gated_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                const void* v, const int64_t* v_strides, const void* gate,
+                                const int64_t* gate_strides, const void* q_norm_w, int q_norm_dtype,
+                                float q_norm_eps, const void* cos_table, const void* sin_table, int rotary_dim,
+                                void* out, int B, int L, int Hq, int Hkv, int d, int block, float scale, int dtype,
+                                int flags, void* stream);
+
+/*
  * Block-causal attention of a query segment against a key/value cache: the clean-prefix cache of a
  * cached decoder. The reference decoder (src/dllm_qwen38/decode.py:63-66) re-runs the whole
  * two-stream forward per denoising step; there, x_t block k sees x_0 blocks < k and itself
@@ -291,7 +314,9 @@ int dllm_swiglu_rows_fwd(const void* gate, const void* up, int64_t ld, void* out
  * rotary_dim dims, out = a*cos + rotate_half(a)*sin with products and sum rounded to the dtype.
  * Token t reads table row t mod L (positions shared by both halves of cat([x_t, x_0]),
  * src/dllm_qwen38/blockdiff.py:143-144). cos/sin [L, rotary_dim] in the activation dtype.
- * Writes contiguous q_out [B,S,Hq,hd], k_out [B,S,Hkv,hd]. hd <= 256.
+ * Writes contiguous q_out [B,S,Hq,hd], k_out [B,S,Hkv,hd]. hd <= 256. Hq = 0: the k rows alone
+ * (q, q_strides, q_norm_w and q_out may be null), for a layer whose q prologue runs inside
+ * dllm_bd_attention_gated_fwd.
  * Replaces [hf]:672-680 (q_norm, k_norm, apply_rotary_pos_emb [hf]:554-589).
  */
 int dllm_qk_norm_rope_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,

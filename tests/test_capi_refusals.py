@@ -68,13 +68,20 @@ def bd(q=P, B=1, L=64, Hq=4, Hkv=2, d=64, block=32, dtype=BF, st_t=256):
             s3(st_t * 2 * L, st_t, d), P, B, L, Hq, Hkv, d, block, 0.125, dtype, 0, None)
 
 
+def gated(q=P, B=1, L=64, Hq=4, Hkv=2, d=256, block=32, dtype=BF, rd=64, qnw=P, gate=P, cos=P, wdt=BF, st_t=1024):
+    """dllm_bd_attention_gated_fwd with the q prologue (qnw) and the gate."""
+    return ("dllm_bd_attention_gated_fwd", q, s3(st_t * 2 * L, st_t, d), P, s3(st_t * 2 * L, st_t, d), P,
+            s3(st_t * 2 * L, st_t, d), gate, s3(st_t * 2 * L, st_t, d) if gate else None, qnw, wdt, 1e-6, cos, P, rd,
+            P, B, L, Hq, Hkv, d, block, 0.0625, dtype, 0, None)
+
+
 def bc(B=1, M=32, N=96, q0=64, Hq=4, Hkv=2, d=64, block=32, ws=None, splits=1):
     return ("dllm_block_causal_attention_fwd", P, s3(M * 256, 256, 64), P, s3(N * 128, 128, 64), P,
             s3(N * 128, 128, 64), P, B, M, N, q0, Hq, Hkv, d, block, 0.125, BF, ws, splits, None)
 
 
-def rope(q=P, B=1, S=8, L=8, Hq=4, Hkv=2, hd=64, rd=16, cos=P, dt=BF, dtw=BF, qst=(2048, 256, 64)):
-    return ("dllm_qk_norm_rope_fwd", q, s3(*qst), P, s3(1024, 128, 64), P, P, cos, P, P, P,
+def rope(q=P, B=1, S=8, L=8, Hq=4, Hkv=2, hd=64, rd=16, cos=P, dt=BF, dtw=BF, qst=(2048, 256, 64), k=P):
+    return ("dllm_qk_norm_rope_fwd", q, s3(*qst), k, s3(1024, 128, 64), P, P, cos, P, P, P,
             B, S, L, Hq, Hkv, hd, rd, 1e-6, dt, dtw, None)
 
 
@@ -133,6 +140,20 @@ CASES = {
     "bd head dim": (bd(d=320, st_t=320), EUNSUP, "head_dim 320 > 256"),
     "bd dtype": (bd(dtype=7), EUNSUP, "dtype 7 not supported"),
     "bd 32-bit extent": (bd(L=1 << 15, st_t=1 << 16), EUNSUP, "32-bit element offsets"),
+    # the gated attention layer's core in one launch ([hf]:672-698)
+    "gated null pointer": (gated(q=None), EINVAL, "gated attention: null pointer"),
+    "gated null table": (gated(cos=None), EINVAL, "null rotary table"),
+    "gated empty": (gated(B=0), EINVAL, "gated attention: bad sizes"),
+    "gated L % block": (gated(L=48), EINVAL, "L=48 is not a multiple of block=32"),
+    "gated head dim 32": (gated(d=32, st_t=128), EUNSUP, "fused form needs bf16"),
+    "gated rotary 32": (gated(rd=32), EUNSUP, "fused form needs bf16"),
+    "gated fp32": (gated(dtype=F32), EUNSUP, "fused form needs bf16"),
+    "gated weight dtype": (gated(wdt=7), EUNSUP, "q norm weight dtype 7"),
+    "gated misaligned q": (gated(q=P2), EUNSUP, "16-byte aligned"),
+    "gated misaligned gate": (gated(gate=P2), EUNSUP, "gate rows must be 8-byte aligned"),
+    "k-only prologue without k": (rope(q=None, Hq=0, k=None), EINVAL, "qk norm rope: null pointer"),
+    "prologue q heads without q": (rope(q=None), EINVAL, "qk norm rope: null pointer"),
+    "prologue negative q heads": (rope(Hq=-1), EINVAL, "qk norm rope: bad sizes"),
     # block-causal attention of the cached decoder (src/dllm_qwen38/decode.py:63-66)
     "bc negative offset": (bc(q0=-1), EINVAL, "bad sizes"),
     "bc offset overflow": (bc(q0=0x7fffffff - 8), EINVAL, "q0 + M overflows"),

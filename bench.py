@@ -142,8 +142,8 @@ def main(argv=None):
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     ap.add_argument("--pieces", type=int, default=None,
                     help="GDN layer workloads: the step's schedule, the layer cut into this many block ranges "
-                         "with the conv of each range beside the fork of the one before (1 = conv, then fork; "
-                         "default 4 at the 27B-class shape, 1 at the 0.8B-class shape, where it measured no gain)")
+                         "with the conv of each range beside the fork of the one before (default 1: conv, then "
+                         "fork, as gdn_state_fork's default; ranges measured no faster)")
     ap.add_argument("--workload", default="gdn-layer",
                     choices=["gdn-layer", "gdn-layer-08b", "gdn-core", "attention", "stack", "decode"],
                     help="gdn-layer (default, the headline metric); gdn-layer-08b: the same layer at the 0.8B-class "
@@ -197,7 +197,7 @@ def _host_info():
 GDN_WORKLOADS = {
     "gdn-layer": ("GDN_27B_BF16", "state-fork GDN layer tokens/s at 27B-class shape; % MFMA/HBM roofline",
                   "state-fork GDN layer, 27B-class: B=4 L=4096 block=chunk=32 Hk=16 Hv=48 Dk=Dv=128 conv width 4, "
-                  "bf16 in/out, fp32 state", "gdn_fork_27b_traffic.json", 4),
+                  "bf16 in/out, fp32 state", "gdn_fork_27b_traffic.json", 1),
     "gdn-layer-08b": ("GDN_08B_BF16", "state-fork GDN layer tokens/s at 0.8B-class shape; % MFMA/HBM roofline",
                       "state-fork GDN layer, 0.8B-class: B=8 L=2048 block=chunk=32 Hk=Hv=16 Dk=Dv=128 conv width 4, "
                       "bf16 in/out, fp32 state", "gdn_fork_08b_traffic.json", 1),

@@ -467,7 +467,6 @@ __device__ __forceinline__ void rope_pairs(Frag<true> (&qf)[D / 32], const bf16*
       const bf16x8 c2 = *(const bf16x8*)(cs + d2), s2 = *(const bf16x8*)(sn + d2);
       bf16x8& x1 = part ? qf[s].hi : qf[s].lo;
       bf16x8& x2 = part ? qf[s + NH].hi : qf[s + NH].lo;
-      __builtin_amdgcn_sched_barrier(0);  // one pair of runs at a time (register pressure)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float a1 = (float)x1[i], a2 = (float)x2[i];
@@ -499,7 +498,6 @@ __device__ __forceinline__ void q_norm_rope(Frag<true> (&qf)[D / 32], const Attn
   for (int s = 0; s < DT; ++s)
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
-      __builtin_amdgcn_sched_barrier(0);  // one 8-element run at a time (register pressure)
       const int d0 = 32 * s + 16 * part + 8 * h;
       float w[8];
       if (a.q_norm_f32) {
@@ -666,16 +664,13 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
   if (swave) {
     // Q^T fragments of the query tile (contiguous d runs)
     F qf[DT];
+    const int qrow = min(r0 + l32, Lq - 1);
     {
-      const int row = min(r0 + l32, Lq - 1);
-      const bf16* qp = qbase + (long long)((BC ? 0 : qh * L) + row) * a.q_st;
+      const bf16* qp = qbase + (long long)((BC ? 0 : qh * L) + qrow) * a.q_st;
 #pragma unroll
       for (int s = 0; s < DT; ++s) {
         qf[s].lo = *(const bf16x8*)(qp + 32 * s + 8 * h);
         qf[s].hi = *(const bf16x8*)(qp + 32 * s + 16 + 8 * h);
-      }
-      if constexpr (!BC) {
-        if (a.q_norm_w) q_norm_rope<D>(qf, a, row, h);  // the row's position within its half
       }
     }
     // keys visible to this lane's query in each half: [vlo, vhi) (empty past the last query)
@@ -768,6 +763,10 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
     wait_vmcnt<0>();  // only the direct loads are counted below
 #pragma unroll
     for (int i = 0; i < KD; ++i) stage_tile(nbeg + i);
+    // the q prologue while the first K tiles travel (its own loads have returned when it ends)
+    if constexpr (!BC) {
+      if (a.q_norm_w) q_norm_rope<D>(qf, a, qrow, h);  // the row's position within its half
+    }
     wait_tiles(min(KD - 2, max(0, nend - (nbeg + 2))));
     __syncthreads();
     f32x16 sa = s_product(nbeg), sb;  // past the last tile: never used
@@ -879,29 +878,41 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
     bf16* op = (bf16*)a.out + (orow * a.Hq + hq) * a.d;
     // the output gate (gated attention, [hf]:698): bf16(bf16(o) * bf16(sigmoid(gate))), the
     // rounding of the separate elementwise product
-    const bf16* gp = nullptr;
-    if constexpr (!BC)
-      if (a.gate) gp = (const bf16*)a.gate + b * a.g_sb + (long long)(qh * L + qi) * a.g_st + (long long)hq * a.g_sh;
+    bool gated = false;
+    if constexpr (!BC) gated = a.gate != nullptr;
+    if (gated) {
+      // every gate value of the row first (in flight together), then the products;
+      // sigmoid(x) = 1 / (1 + 2^(-x log2 e)) from the hardware exp2 and reciprocal, rounded to bf16
+      const bf16* gp = (const bf16*)a.gate + b * a.g_sb + (long long)(qh * L + qi) * a.g_st + (long long)hq * a.g_sh;
+      bf16x4 g4[DT][4];
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
+      for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        bf16x4 o4;
+        for (int m = 0; m < 4; ++m) g4[t][m] = *(const bf16x4*)(gp + 32 * t + 8 * m + 4 * h);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = (bf16)(O[t][4 * m + i] * inv);
-        if (gp) {
-          const bf16x4 g4 = *(const bf16x4*)(gp + 32 * t + 8 * m + 4 * h);
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          bf16x4 o4;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float sg = (float)(bf16)(1.f / (1.f + expf(-(float)g4[i])));
-            o4[i] = (bf16)((float)o4[i] * sg);
+            const float o = (float)(bf16)(O[t][4 * m + i] * inv);
+            const float sg = (float)(bf16)__builtin_amdgcn_rcpf(
+                1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * (float)g4[t][m][i]));
+            o4[i] = (bf16)(o * sg);
           }
+          *(bf16x4*)(op + 32 * t + 8 * m + 4 * h) = o4;
         }
-        *(bf16x4*)(op + 32 * t + 8 * m + 4 * h) = o4;
-      }
-      // one d slice at a time: the gate loads of later slices are not hoisted above this one's
-      // stores (they would hold registers beside the whole accumulator)
-      __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          bf16x4 o4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o4[i] = (bf16)(O[t][4 * m + i] * inv);
+          *(bf16x4*)(op + 32 * t + 8 * m + 4 * h) = o4;
+        }
     }
   }
 }

@@ -350,13 +350,14 @@ def fork_workgroups(cus: int, B: int, Hv: int) -> int:
 
 
 def default_pieces(cus: int, B: int, Hv: int, nb: int) -> int:
-    """Block ranges of gdn_state_fork's default schedule: 4 where the conv beside the fork was
-    measured to pay, i.e. one workgroup per head that leaves compute units free and 64 blocks or
-    more (27B-class layer, B = 4, L = 4096: 850 vs 861 us); else 1. Each extra range costs a launch
-    and its pipeline ramp, more than a short conv hides (B = 1, L = 2048 with the column split:
-    277 vs 241 us)."""
-    wgs = fork_workgroups(cus, B, Hv)
-    return 4 if wgs == B * Hv and wgs < cus and nb >= 64 else 1
+    """Block ranges of gdn_state_fork's default schedule: 1, the conv then the fork as two
+    launches. Ranges (the conv of each range beside the fork of the range before) measured no
+    faster once the fork's outputs went out as 16-byte row runs: at the 27B-class layer (B = 4,
+    L = 4096) 0.839 vs 0.839 ms per step after 30 warm-ups, and, in fresh processes after 5, four
+    ranges 0.879-0.889 ms against 0.882-0.891 ms for one launch each (interleaved, 4 runs each).
+    At B = 1, L = 2048 (the column split) each extra range costs more than the short conv it hides
+    (277 vs 241 us). `pieces` still selects ranges explicitly; every schedule is bit-identical."""
+    return 1
 
 
 def _side_stream(dev: torch.device) -> torch.cuda.Stream:

@@ -16,11 +16,9 @@ def test_fork_workgroups_rule():
 
 
 def test_default_pieces_rule():
-    """Block ranges by default only where they were measured to pay: one workgroup per head with
-    compute units left free, and at least 64 blocks."""
+    """The default schedule is conv then fork, one launch each, at every shape: block ranges beside
+    the conv measured no faster at the 27B-class layer once the fork sped up, and slower where the
+    column split fills the chip."""
     cus = 256
-    assert gdn.default_pieces(cus, 4, 48, 128) == 4   # 27B-class layer, L = 4096
-    assert gdn.default_pieces(cus, 4, 48, 32) == 1    # too few blocks per range
-    assert gdn.default_pieces(cus, 1, 48, 64) == 1    # column split (96 workgroups)
-    assert gdn.default_pieces(cus, 8, 16, 64) == 1    # column split fills the chip
-    assert gdn.default_pieces(cus, 8, 48, 128) == 1   # 384 workgroups: no CU free
+    for B, Hv, nb in ((4, 48, 128), (4, 48, 32), (1, 48, 64), (8, 16, 64), (8, 48, 128)):
+        assert gdn.default_pieces(cus, B, Hv, nb) == 1

@@ -1,9 +1,10 @@
 """The benchmarked GDN layer workloads at their own sizes, against the CPU oracle.
 
-bench.py times the 27B-class layer (B=4, L=4096, Hk=16, Hv=48, D=128, block 32) as 4 block ranges,
-the conv of each range beside the fork of the one before, and the 0.8B-class layer (B=8, L=2048,
-Hk=Hv=16) as one launch whose heads' value columns are split over two workgroups. Here both run
-exactly as the benchmark runs them (StateForkPlan, the bench's seeded inputs), and every output,
+bench.py times the 27B-class layer (B=4, L=4096, Hk=16, Hv=48, D=128, block 32) as the conv
+launch then one fork launch, and the 0.8B-class layer (B=8, L=2048, Hk=Hv=16) as one launch whose
+heads' value columns are split over two workgroups; `--pieces 4` times the 27B-class layer as 4
+block ranges, the conv of each range beside the fork of the one before. Here each runs exactly as
+the benchmark runs it (StateForkPlan, the bench's seeded inputs), and every output,
 state snapshot and conv tail is compared with oracle/gdn_ref.state_fork_layer on the same inputs:
 tails bit-exact, outputs and states within the bf16 bounds of tests/_bounds.py. Each workload is
 checked on its own inputs (25-45 nats of decay per block at the 27B-class shape) and again with
@@ -48,6 +49,7 @@ def _run_like_bench(s, x, dev, pieces):
 
 CASES = [
     # (shape, schedule of the benchmark, g shift)
+    (inputs.GDN_27B_BF16, 1, None),
     (inputs.GDN_27B_BF16, 4, None),
     (inputs.GDN_27B_BF16, 4, inputs.GDN_27B_BF16.g_shift - 4.0),
     (inputs.GDN_08B_BF16, 1, None),
@@ -55,8 +57,8 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("s,pieces,shift", CASES, ids=["27b-4-ranges", "27b-4-ranges-slow-decay", "08b-split",
-                                                        "08b-split-slow-decay"])
+@pytest.mark.parametrize("s,pieces,shift", CASES, ids=["27b-one-launch", "27b-4-ranges", "27b-4-ranges-slow-decay",
+                                                        "08b-split", "08b-split-slow-decay"])
 def test_benchmarked_layer_matches_oracle_at_full_size(dev, s, pieces, shift):
     torch.set_num_threads(len(os.sched_getaffinity(0)))
     x = inputs.gdn_layer_inputs(s, g_shift=shift)

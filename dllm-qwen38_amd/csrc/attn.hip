@@ -542,7 +542,12 @@ struct SpSmem {
 };
 enum { SP_SKIP = 1, SP_RESCALE = 2 };
 
-template <int D, bool BC>
+// TPW: query tiles per workgroup. 4: four consecutive tiles of one query head. 2: two tiles of each
+// of two query heads that share a K/V head (even GQA ratios): the workgroup walks the union of the
+// key tiles its query tiles see, so fewer consecutive tiles waste fewer phases on tiles only some
+// of them see. Every visible tile is walked in the same order either way, so the outputs are the
+// same bits.
+template <int D, bool BC, int TPW = 4>
 __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
   using SM = SpSmem<D>;
   using F = Frag<true>;
@@ -566,25 +571,28 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
   const int Lk = BC ? a.N : L;
   const int qa = BC ? a.q0 : 0;
   const int ntq = (Lq + 31) >> 5;
-  const int ng = (ntq + 3) >> 2;
+  static_assert(TPW == 4 || TPW == 2, "query tiles per workgroup");
+  constexpr int HPW = 4 / TPW;  // query heads per workgroup
+  const int ng = (ntq + TPW - 1) / TPW;
   const int rep = a.Hq / a.Hkv;
+  const int nhu = rep / HPW;    // head units per K/V head
 
-  // work unit: longest first (tile group descending), then half, batch, KV head, query head in group
+  // work unit: longest first (tile group descending), then half, batch, KV head, query heads in group
   constexpr int NH = BC ? 1 : 2;
-  const int lin = attn_unit(blockIdx.x, gridDim.x, NH * rep);
-  const int per_g = NH * a.B * a.Hkv * rep;
+  const int lin = attn_unit(blockIdx.x, gridDim.x, NH * nhu);
+  const int per_g = NH * a.B * a.Hkv * nhu;
   const int g = ng - 1 - lin / per_g;
   int rem = lin % per_g;
   const int qh = BC ? 1 : rem % 2;
   rem /= NH;
-  const int hr = rem % rep;
-  rem /= rep;
+  const int hr = rem % nhu;
+  rem /= nhu;
   const int hkv = rem % a.Hkv;
   const int b = rem / a.Hkv;
-  const int hq = hkv * rep + hr;
+  const int hq = hkv * rep + hr * HPW + pair / TPW;  // this wave pair's query head
 
-  const int g0 = g * 128, g1 = min(Lq, g0 + 128);
-  const int r0 = g0 + pair * 32, r1 = min(Lq, r0 + 32);
+  const int g0 = g * (32 * TPW), g1 = min(Lq, g0 + 32 * TPW);
+  const int r0 = g0 + (pair % TPW) * 32, r1 = min(Lq, r0 + 32);
   const bool wave_live = r0 < Lq;
   const int qb0 = (qa + r0) / C, qb1 = (qa + max(r0, r1 - 1)) / C;
   const int gqb0 = (qa + g0) / C, gqb1 = (qa + g1 - 1) / C;
@@ -946,14 +954,21 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   *(bf16x4*)(out + row * d + c) = r;
 }
 
+#ifndef DLLM_ATTN_GQ
+#define DLLM_ATTN_GQ 1
+#endif
 template <int D, bool BC>
 static int launch_attn_sp(const AttnArgs& a, hipStream_t st) {
   const int ntq = ((BC ? a.M : a.L) + 31) / 32;
-  const int ng = (ntq + 3) / 4;
-  const long long nblk = (long long)ng * (BC ? 1 : 2) * a.B * a.Hq;
+  // two query heads per workgroup where the GQA ratio is even (complementary-mask mode)
+  const bool two = DLLM_ATTN_GQ && !BC && (a.Hq / a.Hkv) % 2 == 0;
+  const int tpw = two ? 2 : 4;
+  const int ng = (ntq + tpw - 1) / tpw;
+  const long long nblk = (long long)ng * (BC ? 1 : 2) * a.B * a.Hq / (4 / tpw);
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "attention: grid too large");
   const int ks = BC && a.ksplit > 1 ? a.ksplit : 1;
-  bd_attn_sp_kernel<D, BC><<<dim3((unsigned)nblk, ks), dim3(512), 0, st>>>(a);
+  if (two) bd_attn_sp_kernel<D, BC, 2><<<dim3((unsigned)nblk, ks), dim3(512), 0, st>>>(a);
+  else bd_attn_sp_kernel<D, BC, 4><<<dim3((unsigned)nblk, ks), dim3(512), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention launch: %s", hipGetErrorString(e));
   if (ks > 1) {

@@ -351,10 +351,11 @@ def fork_workgroups(cus: int, B: int, Hv: int) -> int:
 
 def default_pieces(cus: int, B: int, Hv: int, nb: int) -> int:
     """Block ranges of gdn_state_fork's default schedule: 1, the conv then the fork as two
-    launches. Ranges (the conv of each range beside the fork of the range before) measured no
-    faster once the fork's outputs went out as 16-byte row runs: at the 27B-class layer (B = 4,
-    L = 4096) 0.839 vs 0.839 ms per step after 30 warm-ups, and, in fresh processes after 5, four
-    ranges 0.879-0.889 ms against 0.882-0.891 ms for one launch each (interleaved, 4 runs each).
+    launches. Ranges (the conv of each range beside the fork of the range before) measured within
+    the clock spread of it once the fork's outputs went out as 16-byte row runs: at the 27B-class
+    layer (B = 4, L = 4096) four ranges 0.838-0.841 ms per step against 0.846-0.847 ms after 30
+    warm-ups, and, in fresh processes after 5, 0.879-0.889 ms against 0.882-0.891 ms (interleaved,
+    4 runs each), where the schedule timed first is the one the clock ramp penalises.
     At B = 1, L = 2048 (the column split) each extra range costs more than the short conv it hides
     (277 vs 241 us). `pieces` still selects ranges explicitly; every schedule is bit-identical."""
     return 1

@@ -954,14 +954,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   *(bf16x4*)(out + row * d + c) = r;
 }
 
-#ifndef DLLM_ATTN_GQ
-#define DLLM_ATTN_GQ 1
-#endif
 template <int D, bool BC>
 static int launch_attn_sp(const AttnArgs& a, hipStream_t st) {
   const int ntq = ((BC ? a.M : a.L) + 31) / 32;
-  // two query heads per workgroup where the GQA ratio is even (complementary-mask mode)
-  const bool two = DLLM_ATTN_GQ && !BC && (a.Hq / a.Hkv) % 2 == 0;
+  // two query heads per workgroup where the GQA ratio is even (complementary-mask mode; measured
+  // 911.6 vs 947.2 us at B=2 L=4096 Hq=24 Hkv=4 d=256, bit-identical)
+  const bool two = !BC && (a.Hq / a.Hkv) % 2 == 0;
   const int tpw = two ? 2 : 4;
   const int ng = (ntq + tpw - 1) / tpw;
   const long long nblk = (long long)ng * (BC ? 1 : 2) * a.B * a.Hq / (4 / tpw);

@@ -547,6 +547,11 @@ extern "C" int dllm_qk_norm_rope_fwd(const void* q, const int64_t* q_strides, co
         (const bf16*)q, q_strides[0], (int)q_strides[1], (int)q_strides[2], (const bf16*)k, k_strides[0],
         (int)k_strides[1], (int)k_strides[2], (const bf16*)q_norm_w, (const bf16*)k_norm_w, (const bf16*)cos_table,
         (const bf16*)sin_table, (bf16*)q_out, (bf16*)k_out, B, S, L, Hq, Hkv, head_dim, rotary_dim, eps);
+  else if (dtype == DT_BF16 && dtype_w == DT_F32)  // norm weights kept in fp32 beside bf16 activations
+    qk_norm_rope_kernel<bf16, float><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
+        (const bf16*)q, q_strides[0], (int)q_strides[1], (int)q_strides[2], (const bf16*)k, k_strides[0],
+        (int)k_strides[1], (int)k_strides[2], (const float*)q_norm_w, (const float*)k_norm_w, (const bf16*)cos_table,
+        (const bf16*)sin_table, (bf16*)q_out, (bf16*)k_out, B, S, L, Hq, Hkv, head_dim, rotary_dim, eps);
   else if (dtype == DT_F32 && dtype_w == DT_F32)
     qk_norm_rope_kernel<float, float><<<dim3((unsigned)nb), dim3(256), 0, st>>>(
         (const float*)q, q_strides[0], (int)q_strides[1], (int)q_strides[2], (const float*)k, k_strides[0],

@@ -314,7 +314,8 @@ int dllm_swiglu_rows_fwd(const void* gate, const void* up, int64_t ld, void* out
  * rotary_dim dims, out = a*cos + rotate_half(a)*sin with products and sum rounded to the dtype.
  * Token t reads table row t mod L (positions shared by both halves of cat([x_t, x_0]),
  * src/dllm_qwen38/blockdiff.py:143-144). cos/sin [L, rotary_dim] in the activation dtype.
- * Writes contiguous q_out [B,S,Hq,hd], k_out [B,S,Hkv,hd]. hd <= 256. Hq = 0: the k rows alone
+ * Writes contiguous q_out [B,S,Hq,hd], k_out [B,S,Hkv,hd]. hd <= 256. dtype / dtype_w: bf16 / bf16,
+ * bf16 / fp32 (norm weights kept in fp32) or fp32 / fp32. Hq = 0: the k rows alone
  * (q, q_strides, q_norm_w and q_out may be null), for a layer whose q prologue runs inside
  * dllm_bd_attention_gated_fwd.
  * Replaces [hf]:672-680 (q_norm, k_norm, apply_rotary_pos_emb [hf]:554-589).

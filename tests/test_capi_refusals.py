@@ -187,7 +187,7 @@ CASES = {
     "rope head dim": (rope(hd=512, rd=16), EINVAL, "bad sizes"),
     "rope tables missing": (rope(cos=None), EINVAL, "null rotary table"),
     "rope 32-bit strides": (rope(qst=(1 << 40, 1 << 32, 64)), EUNSUP, "strides exceed 32 bits"),
-    "rope dtype pair": (rope(dtw=F32), EUNSUP, "dtype pair (1, 0) not supported"),
+    "rope dtype pair": (rope(dt=F32, dtw=BF), EUNSUP, "dtype pair (0, 1) not supported"),
     # decoding-step projections
     "linear no projections": (multi(count=0), EINVAL, "0 projections"),
     "linear five projections": (multi(count=5, Ns=(128,) * 5), EINVAL, "5 projections"),

@@ -6,9 +6,11 @@ as it stores the output ([hf]:672-698 around the complementary-mask attention).
     attn_ref.bd_attention, sigmoid gate), within the bf16 attention bar of tests/test_gpu_attn.py
     (2^-8 max|V| + 2^-7 |ref|) scaled by the gate (|sigmoid| < 1) plus one bf16 ulp of the product;
   * against the separate launches (qk_norm_rope, bd_attention, torch's sigmoid product) on the
-    same inputs: within two bf16 ulps per element. The two kernels sum a q row's squares in
-    different orders, so 1/rms may differ in its last bit; that flips the rounding of an occasional
-    normalised q element, and through the scores every output of that row moves by about an ulp;
+    same inputs: within two bf16 ulps per element where the separate prologue is the 256-wide bf16
+    kernel. The two kernels sum a q row's squares in different orders, so 1/rms may differ in its
+    last bit; that flips the rounding of an occasional normalised q element, and through the
+    scores every output of that row moves by about an ulp. Against the generic prologue kernel
+    (other head sizes, fp32 norm weights), whose order differs for most rows, within the oracle bar;
   * the k-only prologue equals the k output of the two-tensor prologue bit for bit.
 """
 
@@ -33,30 +35,33 @@ def _tables(L, rd, dtype):
     return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
-def _inputs(B, L, Hq, Hkv, d, rd, seed):
+def _inputs(B, L, Hq, Hkv, d, rd, seed, wdtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     S = 2 * L
     qg = torch.randn(B, S, Hq, 2 * d, generator=g).to(torch.bfloat16)  # q_proj output: query | gate per head
     k = torch.randn(B, S, Hkv, d, generator=g).to(torch.bfloat16)
     v = torch.randn(B, S, Hkv, d, generator=g).to(torch.bfloat16)
-    wq = (0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
-    wk = (0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    wq = (0.1 * torch.randn(d, generator=g)).to(wdtype)
+    wk = (0.1 * torch.randn(d, generator=g)).to(wdtype)
     cos, sin = _tables(L, rd, torch.bfloat16)
     return qg, k, v, wq, wk, cos, sin
 
 
-CASES = [  # B, L, Hq, Hkv, d, rd, block, leak
-    (1, 128, 6, 2, 256, 64, 32, False),   # the 27B-class attention layer's head geometry
-    (2, 96, 4, 1, 256, 128, 32, False),
-    (1, 64, 4, 2, 128, 64, 16, False),
-    (1, 64, 2, 2, 64, 64, 8, False),
-    (1, 128, 6, 2, 256, 64, 32, True),    # the mask-leak fault
+CASES = [  # B, L, Hq, Hkv, d, rd, block, leak, norm weight dtype
+    (1, 128, 6, 2, 256, 64, 32, False, torch.bfloat16),   # the 27B-class attention layer's head geometry
+    (2, 96, 4, 1, 256, 128, 32, False, torch.bfloat16),
+    (1, 64, 4, 2, 128, 64, 16, False, torch.bfloat16),
+    (1, 64, 2, 2, 64, 64, 8, False, torch.bfloat16),
+    (1, 128, 6, 2, 256, 64, 32, True, torch.bfloat16),    # the mask-leak fault
+    (1, 64, 4, 2, 256, 192, 32, False, torch.float32),    # three rotated slice pairs, fp32 norm weights
+    (1, 96, 2, 1, 256, 256, 32, False, torch.bfloat16),   # the whole head rotated
+    (2, 64, 4, 2, 128, 128, 32, False, torch.float32),
 ]
 
 
-@pytest.mark.parametrize("B,L,Hq,Hkv,d,rd,block,leak", CASES)
-def test_gated_attention_one_launch(dev, B, L, Hq, Hkv, d, rd, block, leak):
-    qg, k, v, wq, wk, cos, sin = _inputs(B, L, Hq, Hkv, d, rd, seed=91 + d + rd + L)
+@pytest.mark.parametrize("B,L,Hq,Hkv,d,rd,block,leak,wdtype", CASES)
+def test_gated_attention_one_launch(dev, B, L, Hq, Hkv, d, rd, block, leak, wdtype):
+    qg, k, v, wq, wk, cos, sin = _inputs(B, L, Hq, Hkv, d, rd, seed=91 + d + rd + L, wdtype=wdtype)
     S = 2 * L
     qgd = qg.to(dev)
     q, gate = qgd[..., :d], qgd[..., d:]  # strided views, as the layer passes them
@@ -84,10 +89,18 @@ def test_gated_attention_one_launch(dev, B, L, Hq, Hkv, d, rd, block, leak):
         assert (err <= bar).all(), name
     diff = (got.float() - sep.float()).abs().cpu()
     frac = (diff > 0).float().mean().item()
-    two_ulps = 2 ** -6 * sep.float().abs().cpu() + 2 ** -9 * sep.float().abs().max().item()
+    if d == 256 and wdtype == torch.bfloat16:
+        # the separate prologue is the 256-wide bf16 kernel, whose row sums the fused load matches
+        # but for an occasional last bit: within two bf16 ulps per element
+        cross = 2 ** -6 * sep.float().abs().cpu() + 2 ** -9 * sep.float().abs().max().item()
+    else:
+        # the generic prologue kernel sums a row's squares in another order, so 1/rms differs in its
+        # last bit for most rows and normalised q elements round differently throughout the tile:
+        # the two launches then agree only as well as each agrees with the oracle (the same bar)
+        cross = bar
     print(f"one launch vs separate launches: {frac:.2%} of elements differ, max|d|={diff.max().item():.3e}, "
-          f"max |d|/two ulps={(diff / two_ulps).max().item():.3f}")
-    assert (diff <= two_ulps).all()
+          f"max |d|/bound={(diff / cross).max().item():.3f}")
+    assert (diff <= cross).all()
     assert got.shape == (B, S, Hq, d) and got.is_contiguous()
 
 

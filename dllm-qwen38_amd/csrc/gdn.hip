@@ -843,6 +843,17 @@ enum { VP_GAML = 0, VP_EG = 32 };
 enum { STATUS_LDS_WAIT = 1u };
 static __device__ unsigned dllm_status_word;
 
+// One fp32 element of a state snapshot: a non-temporal store (nothing in the launch reads the
+// snapshot back) at device scope, so that the line is written through to memory instead of held
+// dirty in the XCD's L2 until the launch ends. Issued as its own instruction, which also keeps the
+// compiler from moving the stores among the update's products. Measured at the 27B-class layer:
+// the fork 559.6 vs 594.3 us with the compiler's non-temporal store (571.2 us for the same nt
+// store issued this way, 562.3 us with system scope), bit-identical; 253.1 vs 259.2 us at the
+// 0.8B-class layer.
+__device__ __forceinline__ void store_snapshot(float* p, float v) {
+  asm volatile("global_store_dword %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+}
+
 __device__ __forceinline__ void report_status(unsigned bit) {
   __hip_atomic_fetch_or(&dllm_status_word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1423,8 +1434,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
             mma32(S[kt], fku[kt], fd);
             if (sb) {
 #pragma unroll
-              for (int v = 0; v < 16; ++v)
-                __builtin_nontemporal_store(S[kt][v], sb + (32 * kt + v) * 128);
+              for (int v = 0; v < 16; ++v) store_snapshot(sb + (32 * kt + v) * 128, S[kt][v]);
             }
           }
         }

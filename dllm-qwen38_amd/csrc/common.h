@@ -131,6 +131,13 @@ __device__ __forceinline__ void dma_load16(const void* src, const void* lds_base
   const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_cptr)lds_base);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
 }
+// The same for data read once per launch and never again soon (streamed weights): non-temporal
+// at device scope, so the lines do not displace reused data in the L2 and the last-level cache.
+__device__ __forceinline__ void dma_load16_stream(const void* src, const void* lds_base) {
+  typedef const __attribute__((address_space(3))) void* lds_cptr;
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_cptr)lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt sc1" ::"v"(src), "s"(m0) : "memory", "m0");
+}
 
 // Ordering point for LDS traffic between lanes of ONE wavefront (no s_barrier): LDS operations of
 // a wave complete in issue order, so only compiler reordering has to be prevented.

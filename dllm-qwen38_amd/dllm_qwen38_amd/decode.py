@@ -112,13 +112,34 @@ def generate(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int, block
     return trace
 
 
+_WORKSPACES: dict = {}
+_SIZES: dict = {}
+
+
+def _workgroups(L, M: int, N: int, K: int) -> int:
+    key = ("g", M, N, K)
+    G = _SIZES.get(key)
+    if G is None:
+        G = _SIZES[key] = L.dllm_decode_linear_workgroups(M, N, K)
+    return G
+
+
 def _workspace(L, M: int, n_gate: int, G: int, swiglu: bool, dev) -> torch.Tensor:
     """Workspace of one decoding-step projection launch: the fp32 pieces of the tiles split between
-    workgroups (and with swiglu the up projection's rounded tiles)."""
-    nbytes = L.dllm_decode_linear_workspace_bytes(M, n_gate, G, int(swiglu))
+    workgroups (and with swiglu the up projection's rounded tiles). One buffer per (device, stream,
+    size), reused: launches on one stream run in order, and a launch's pieces are consumed by its
+    own second kernel before the next launch on that stream writes them."""
+    key = ("w", M, n_gate, G, bool(swiglu))
+    nbytes = _SIZES.get(key)
+    if nbytes is None:
+        nbytes = _SIZES[key] = L.dllm_decode_linear_workspace_bytes(M, n_gate, G, int(swiglu))
     if nbytes <= 0:
         raise ValueError(f"decode linear: no workspace size for M={M} workgroups={G}")
-    return torch.empty(-(-nbytes // 16) * 4, dtype=torch.float32, device=dev)
+    wkey = (dev.index, _lib.stream_handle(dev), nbytes)
+    ws = _WORKSPACES.get(wkey)
+    if ws is None:
+        ws = _WORKSPACES[wkey] = torch.empty(-(-nbytes // 16) * 4, dtype=torch.float32, device=dev)
+    return ws
 
 
 def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -136,7 +157,7 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | 
     w = weight.contiguous()
     M = x2.shape[0]
     L = _lib.lib()
-    G = L.dllm_decode_linear_workgroups(M, N, K)
+    G = _workgroups(L, M, N, K)
     if G <= 0:
         raise ValueError(f"decode_linear does not take M={M} N={N} K={K} (M <= 64, K % 64 == 0)")
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev) if out is None else out
@@ -165,7 +186,7 @@ def decode_linear_multi(x: torch.Tensor, weights: list, *, swiglu: bool = False)
     if swiglu and (len(ws) != 2 or Ns[0] != Ns[1]):
         raise ValueError("swiglu takes (gate, up) of equal N")
     L = _lib.lib()
-    G = L.dllm_decode_linear_workgroups(M, sum(-(-n // 128) * 128 for n in Ns), K)
+    G = _workgroups(L, M, sum(-(-n // 128) * 128 for n in Ns), K)
     if G <= 0:
         raise ValueError(f"decode_linear_multi does not take M={M} K={K} (M <= 64, K % 64 == 0)")
     outs = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in (Ns[:1] if swiglu else Ns)]

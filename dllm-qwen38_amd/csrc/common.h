@@ -49,6 +49,13 @@ template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf
 // Round an fp32 value through type T (identity for float).
 template <typename T> __device__ __forceinline__ float round_through(float x) { return to_f32(from_f32<T>(x)); }
 
+// Sum over the 64 lanes of a wave, returned to every lane (butterfly: strides 32, 16, .., 1).
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
 // SiLU x * sigmoid(x) from the hardware base-2 exponential and reciprocal (each within 1 ulp):
 // within a few fp32 ulp of x / (1 + e^-x); large negative x gives -0 where the exact value underflows.
 __device__ __forceinline__ float silu_f32(float x) {

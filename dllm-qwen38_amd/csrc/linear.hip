@@ -31,6 +31,7 @@
 //     (gate | up) the second kernel writes round(round(silu(gate)) * up), the MLP's activation,
 //     over the whole gate projection (whole tiles were stored rounded, the up tiles in the
 //     workspace).
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -262,6 +263,104 @@ __global__ __launch_bounds__(256) void decode_linear_swiglu_kernel(LinArgs a) {
   }
 }
 
+// The end of a projection fused with the residual add and RMSNorm that follow it (the decoder's
+// out_proj / o_proj and down_proj, then the next norm), in place of the fixup launch and the norm's
+// own: one workgroup per token row m.
+//   1. Every thread forms the rounded projection values of 4-feature slots q = tid, tid + blockDim,
+//      ..: the tile's stored value (seg[0].y) or, for a tile split between workgroups, the sum of
+//      its pieces in workgroup order, rounded (the fixup's arithmetic; the pieces' loads go out
+//      eight at a time before their sums), into an LDS row of bf16 (exact: the values are rounded).
+//   2. The first nw waves run the row RMSNorm kernel's arithmetic on that row: lane vectors of 8
+//      features (vector k nw + wave, lane), s = round(y + r) written to sum_out, sums of squares in
+//      lane, wave and wave-order, out = round(s rsqrt(mean(s^2) + eps) (1 + w)) (w as is with
+//      unit = 0). Their residual and weight loads are issued before step 1.
+template <typename TW, int NVW>
+__global__ __launch_bounds__(1024) void decode_linear_rmsnorm_kernel(LinArgs a, const bf16* __restrict__ r,
+                                                                     bf16* __restrict__ sum_out,
+                                                                     const TW* __restrict__ w, bf16* __restrict__ out,
+                                                                     float eps, int unit, int nw) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lin_rms_smem[];
+  bf16* const yrow = (bf16*)lin_rms_smem;  // [N]
+  float* const part = (float*)(lin_rms_smem + (size_t)a.seg[0].N * sizeof(bf16));  // [8]
+  typedef __attribute__((ext_vector_type(8))) TW W8;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int m = blockIdx.x, mt = m >> 5, mr = m & 31;
+  const int N = a.seg[0].N;
+  const long long base = (long long)m * N;
+  const bool norm_wave = wv < nw;
+  bf16x8 rv[NVW];
+  W8 wt[NVW];
+  if (norm_wave) {
+#pragma unroll
+    for (int k = 0; k < NVW; ++k) {
+      const int c0 = ((k * nw + wv) * 64 + lane) * 8;
+      wt[k] = *(const W8*)(w + c0);
+      rv[k] = *(const bf16x8*)(r + base + c0);
+    }
+  }
+  for (int q = threadIdx.x; q < N / 4; q += blockDim.x) {
+    const int c = 4 * q;
+    const int t0 = (mt * a.ntn + (c >> 7)) * a.ns;
+    const int w0 = lin_owner(a, t0), w1 = lin_owner(a, t0 + a.ns - 1);
+    bf16x4 yv;
+    if (w0 == w1) {
+      yv = *(const bf16x4*)(a.seg[0].y + base + c);
+    } else {
+      const float* const p = a.part + mr * 128 + (c & 127);
+      f32x4 sum = *(const f32x4*)(p + (long long)(2 * w0 + (lin_start(a, w0) >= t0 ? 0 : 1)) * LIN_TILE);
+      for (int wb = w0 + 1; wb <= w1; wb += 8) {
+        f32x4 pc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (wb + i <= w1) pc[i] = *(const f32x4*)(p + (long long)(2 * (wb + i)) * LIN_TILE);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (wb + i <= w1) sum += pc[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) yv[i] = (bf16)sum[i];
+    }
+    *(bf16x4*)(yrow + c) = yv;
+  }
+  __syncthreads();
+  float v[NVW][8];
+  if (norm_wave) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NVW; ++k) {
+      const int c0 = ((k * nw + wv) * 64 + lane) * 8;
+      const bf16x8 yv = *(const bf16x8*)(yrow + c0);
+      bf16x8 sv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = (bf16)((float)yv[i] + (float)rv[k][i]);
+      *(bf16x8*)(sum_out + base + c0) = sv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[k][i] = (float)sv[i];
+        ss = __builtin_fmaf(v[k][i], v[k][i], ss);
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) part[wv] = ss;
+  }
+  __syncthreads();
+  if (!norm_wave) return;
+  float tot = part[0];
+  for (int i = 1; i < nw; ++i) tot += part[i];
+  const float inv = rsqrtf(tot / (float)N + eps);
+#pragma unroll
+  for (int k = 0; k < NVW; ++k) {
+    const int c0 = ((k * nw + wv) * 64 + lane) * 8;
+    bf16x8 yv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float wf = to_f32(wt[k][i]);
+      yv[i] = (bf16)(v[k][i] * inv * (unit ? 1.f + wf : wf));
+    }
+    *(bf16x8*)(out + base + c0) = yv;
+  }
+}
+
 }  // namespace dllm
 
 using namespace dllm;
@@ -286,9 +385,11 @@ extern "C" long long dllm_decode_linear_workspace_bytes(int M, int N_gate, int w
   return b;
 }
 
-extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const void* const* weights,
-                                            void* const* outs, const int* Ns, void* workspace, int workgroups,
-                                            int swiglu, int dtype, void* stream) {
+// Checks the arguments, fills `a` and launches the streaming kernel (every entry point's first
+// launch); the caller launches what sums the split tiles.
+static int lin_launch_main(const void* x, int M, int K, int count, const void* const* weights, void* const* outs,
+                           const int* Ns, void* workspace, int workgroups, int swiglu, int dtype, hipStream_t st,
+                           LinArgs& a) {
   if (!x || !weights || !outs || !Ns) return fail(DLLM_EINVAL, "decode linear: null pointer");
   if (count < 1 || count > LIN_MAXSEG) return fail(DLLM_EINVAL, "decode linear: %d projections (1..%d)", count, LIN_MAXSEG);
   if (M <= 0 || K <= 0 || workgroups <= 0) return fail(DLLM_EINVAL, "decode linear: bad sizes M=%d K=%d", M, K);
@@ -298,7 +399,7 @@ extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int cou
   if ((uintptr_t)x & 15) return fail(DLLM_EINVAL, "decode linear: x must be 16-byte aligned");
   if (swiglu && (count != 2 || Ns[0] != Ns[1])) return fail(DLLM_EINVAL, "decode linear: swiglu takes gate | up of equal N");
   if (!workspace || ((uintptr_t)workspace & 15)) return fail(DLLM_EINVAL, "decode linear: the workspace must be a 16-byte aligned buffer");
-  LinArgs a = {};
+  a = LinArgs{};
   a.x = (const bf16*)x;
   a.nseg = count;
   a.M = M; a.K = K;
@@ -325,10 +426,20 @@ extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int cou
   a.ur = a.units % a.G;
   a.part = (float*)workspace;
   a.up = swiglu ? (bf16*)((char*)workspace + (long long)a.G * 2 * LIN_TILE * sizeof(float)) : nullptr;
-  hipStream_t st = (hipStream_t)stream;
   decode_linear_kernel<<<dim3((unsigned)a.G), 256, 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear launch: %s", hipGetErrorString(e));
+  return DLLM_OK;
+}
+
+extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const void* const* weights,
+                                            void* const* outs, const int* Ns, void* workspace, int workgroups,
+                                            int swiglu, int dtype, void* stream) {
+  LinArgs a;
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = lin_launch_main(x, M, K, count, weights, outs, Ns, workspace, workgroups, swiglu, dtype, st, a);
+  if (rc != DLLM_OK) return rc;
+  hipError_t e = hipSuccess;
   if (swiglu) {
     decode_linear_swiglu_kernel<<<dim3((unsigned)(a.seg[1].tile0 * ((M + 31) / 32)), LIN_FIX_CHUNKS), 256, 0, st>>>(a);
   } else {
@@ -349,6 +460,62 @@ extern "C" int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int cou
   }
   e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear fixup launch: %s", hipGetErrorString(e));
+  return DLLM_OK;
+}
+
+extern "C" int dllm_decode_linear_rmsnorm_fwd(const void* x, const void* weight, void* workspace, int M, int N, int K,
+                                              int workgroups, const void* residual, void* sum_out,
+                                              const void* norm_weight, void* y, float eps, int unit_offset, int dtype,
+                                              int dtype_w, void* stream) {
+  if (!residual || !sum_out || !norm_weight || !y) return fail(DLLM_EINVAL, "decode linear rmsnorm: null pointer");
+  if (dtype_w != DT_BF16 && dtype_w != DT_F32)
+    return fail(DLLM_EUNSUPPORTED, "decode linear rmsnorm: norm weight dtype %d (bf16 or fp32)", dtype_w);
+  // up to 8192: the widths the row RMSNorm kernel's vector layout covers (the row of rounded
+  // values in LDS is then at most 16 KB)
+  if (N <= 0 || N % 512 || N > 8192)
+    return fail(DLLM_EUNSUPPORTED, "decode linear rmsnorm: N=%d is not a multiple of 512 up to 8192", N);
+  if (((uintptr_t)residual | (uintptr_t)sum_out | (uintptr_t)norm_weight | (uintptr_t)y) & 15)
+    return fail(DLLM_EINVAL, "decode linear rmsnorm: residual, sum_out, norm weight and y must be 16-byte aligned");
+  if (M <= 0 || workgroups <= 0) return fail(DLLM_EINVAL, "decode linear rmsnorm: bad sizes M=%d workgroups=%d", M, workgroups);
+  // the row layout of the row RMSNorm kernel: nw waves (the most, up to 8, dividing N / 512)
+  const int nv = N / 512;
+  int nw = 8;
+  while (nv % nw) --nw;
+  const int nvw = nv / nw;
+  if (nvw > 8) return fail(DLLM_EUNSUPPORTED, "decode linear rmsnorm: N=%d needs %d vectors per lane (at most 8)", N, nvw);
+  // the projection's whole tiles, rounded, go to the workspace after the pieces (the size of
+  // dllm_decode_linear_workspace_bytes(M, N, workgroups, 1))
+  void* proj = (char*)workspace + (long long)workgroups * 2 * LIN_TILE * sizeof(float);
+  const void* w[1] = {weight};
+  void* o[1] = {proj};
+  const int n[1] = {N};
+  LinArgs a;
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = lin_launch_main(x, M, K, 1, w, o, n, workspace, workgroups, 0, dtype, st, a);
+  if (rc != DLLM_OK) return rc;
+  // one thread per 4-feature slot (at most 1024, at least the norm's waves)
+  const int threads = std::min(1024, std::max(64 * nw, (N / 4 + 63) / 64 * 64));
+  const dim3 grid((unsigned)M), block((unsigned)threads);
+  const size_t lds = (size_t)N * sizeof(bf16) + 8 * sizeof(float);
+  const bf16* r = (const bf16*)residual;
+  bf16* so = (bf16*)sum_out;
+  bf16* yo = (bf16*)y;
+  switch (nvw) {
+#define DLLM_LIN_RMS_CASE(NV)                                                                                     \
+  case NV:                                                                                                        \
+    if (dtype_w == DT_BF16)                                                                                       \
+      decode_linear_rmsnorm_kernel<bf16, NV><<<grid, block, lds, st>>>(a, r, so, (const bf16*)norm_weight, yo, eps, \
+                                                                      unit_offset, nw);                           \
+    else                                                                                                          \
+      decode_linear_rmsnorm_kernel<float, NV><<<grid, block, lds, st>>>(a, r, so, (const float*)norm_weight, yo,   \
+                                                                       eps, unit_offset, nw);                     \
+    break;
+    DLLM_LIN_RMS_CASE(1) DLLM_LIN_RMS_CASE(2) DLLM_LIN_RMS_CASE(3) DLLM_LIN_RMS_CASE(4) DLLM_LIN_RMS_CASE(5)
+    DLLM_LIN_RMS_CASE(6) DLLM_LIN_RMS_CASE(7) DLLM_LIN_RMS_CASE(8)
+#undef DLLM_LIN_RMS_CASE
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear rmsnorm launch: %s", hipGetErrorString(e));
   return DLLM_OK;
 }
 

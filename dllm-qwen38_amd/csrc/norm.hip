@@ -10,12 +10,6 @@
 
 namespace dllm {
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
 template <typename T> __device__ __forceinline__ float ld(const T* p) { return to_f32(*p); }
 
 // y = rmsnorm(s) * (1 + w) with s = x (+ r, rounded to T, also written to sum_out)

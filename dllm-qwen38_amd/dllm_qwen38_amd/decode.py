@@ -126,7 +126,8 @@ def _workgroups(L, M: int, N: int, K: int) -> int:
 
 def _workspace(L, M: int, n_gate: int, G: int, swiglu: bool, dev) -> torch.Tensor:
     """Workspace of one decoding-step projection launch: the fp32 pieces of the tiles split between
-    workgroups (and with swiglu the up projection's rounded tiles). One buffer per (device, stream,
+    workgroups (and with swiglu the up projection's rounded tiles; for the fused residual norm the
+    projection's rounded tiles, the same size with n_gate = N). One buffer per (device, stream,
     size), reused: launches on one stream run in order, and a launch's pieces are consumed by its
     own second kernel before the next launch on that stream writes them."""
     key = ("w", M, n_gate, G, bool(swiglu))
@@ -206,6 +207,44 @@ def decode_linear_multi(x: torch.Tensor, weights: list, *, swiglu: bool = False)
     return [o.reshape(*lead, nn) for o, nn in zip(outs, Ns)]
 
 
+def decode_linear_rmsnorm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
+                          eps: float, *, unit_offset: bool = True):
+    """A decoding-step projection followed by the residual add and RMSNorm after it: with
+    p = x @ weight^T rounded to bf16, returns (rmsnorm(s) * (1 + norm_weight), s) where s = p +
+    residual rounded to bf16. Equal element for element to `decode_linear` then
+    `norms.rmsnorm(.., residual=residual)`, in one streaming launch and one row-wise launch (the
+    split tiles' sums, the add and the norm) instead of three. x [..., K] and weight [N, K] bf16 (at
+    most 64 rows, K a multiple of 64), residual [..., N] bf16, norm_weight [N] bf16 or fp32, N a
+    multiple of 512 up to 8192."""
+    dev = _lib.require_device(x, weight, residual, norm_weight)
+    K = x.shape[-1]
+    N = weight.shape[0]
+    if weight.dim() != 2 or weight.shape[1] != K:
+        raise ValueError(f"weight must be [N, {K}], got {tuple(weight.shape)}")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16:
+        raise TypeError("decode_linear_rmsnorm takes bf16 x, weight and residual")
+    lead = x.shape[:-1]
+    if tuple(residual.shape) != (*lead, N) or tuple(norm_weight.shape) != (N,):
+        raise ValueError(f"residual must be {(*lead, N)} and norm_weight ({N},)")
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    L = _lib.lib()
+    G = _workgroups(L, M, N, K)
+    if G <= 0:
+        raise ValueError(f"decode_linear_rmsnorm does not take M={M} N={N} K={K} (M <= 64, K % 64 == 0)")
+    wt = weight.contiguous()
+    r = residual.reshape(M, N).contiguous()
+    w = norm_weight.contiguous()
+    s = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ws = _workspace(L, M, N, G, True, dev)  # the pieces, then the projection's whole tiles
+    _lib.check(L.dllm_decode_linear_rmsnorm_fwd(
+        x2.data_ptr(), wt.data_ptr(), ws.data_ptr(), M, N, K, G, r.data_ptr(), s.data_ptr(),
+        w.data_ptr(), y.data_ptr(), float(eps), int(unit_offset), _lib.dtype_code(x.dtype), _lib.dtype_code(w.dtype),
+        _lib.stream_handle(dev)), "dllm_decode_linear_rmsnorm_fwd")
+    return y.reshape(*lead, N), s.reshape(*lead, N)
+
+
 def _fast(lins, x: torch.Tensor) -> bool:
     """Whether the decoding-step kernels take these projections of x (bf16 rows <= 64, no bias)."""
     rows = x.numel() // x.shape[-1]
@@ -232,14 +271,39 @@ def _proj(lin, x: torch.Tensor) -> torch.Tensor:
     return lin(x)
 
 
-def _mlp(m, x: torch.Tensor) -> torch.Tensor:
-    """SwiGLU MLP ([hf]:704-717): gate and up in one launch with the activation in its reduction,
-    then the down projection."""
+def _norm_width_fused(N: int) -> bool:
+    """Whether dllm_decode_linear_rmsnorm_fwd takes rows of N features: N a multiple of 512 up to
+    8192 whose 512-feature vectors split over at most 8 waves with at most 8 vectors per lane (the
+    row RMSNorm kernel's layout)."""
+    if N <= 0 or N % 512 or N > 8192:
+        return False
+    nv = N // 512
+    nw = max(d for d in range(1, 9) if nv % d == 0)
+    return nv // nw <= 8
+
+
+def _proj_norm(lin, a: torch.Tensor, norm, h: torch.Tensor):
+    """nn.Linear `lin` on a, then the residual add of h and RMSNorm `norm` ([hf]:778-792): returns
+    (norm(lin(a) + h), lin(a) + h). One fused launch pair on the decoding-step kernels
+    (`decode_linear_rmsnorm`), else the projection and the norm kernel."""
+    w = lin.weight
+    rows = a.numel() // a.shape[-1]
+    if (lin.bias is None and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and h.dtype == torch.bfloat16
+            and rows <= 64 and w.shape[1] % 64 == 0 and _norm_width_fused(w.shape[0])
+            and norm.weight.dtype in (torch.bfloat16, torch.float32)):
+        return decode_linear_rmsnorm(a, w, h, norm.weight, _eps(norm))
+    return rmsnorm(_proj(lin, a), norm, residual=h)
+
+
+def _mlp_act(m, x: torch.Tensor):
+    """SwiGLU MLP ([hf]:704-717) up to its down projection: gate and up in one launch with the
+    activation in its reduction. Returns (down_proj, activation): the caller applies down_proj
+    together with the residual add and norm that follow it."""
     if _fast((m.gate_proj, m.up_proj), x):
         act = decode_linear_multi(x, [m.gate_proj.weight, m.up_proj.weight], swiglu=True)
     else:
         act = norms.swiglu(m.gate_proj(x), m.up_proj(x))
-    return _proj(m.down_proj, act)
+    return m.down_proj, act
 
 
 class PrefixCache:
@@ -312,13 +376,13 @@ def _gdn_segment(m, x: torch.Tensor, cache: PrefixCache, i: int, commit: bool) -
         cache.state[i] = states[:, -1].contiguous()
     Dv = m.head_v_dim
     o = norms.gated_rmsnorm(core.reshape(-1, Dv), z.reshape(-1, Dv), m.norm.weight, _eps(m.norm))
-    return _proj(m.out_proj, o.reshape(B, T, -1))
+    return m.out_proj, o.reshape(B, T, -1)
 
 
 def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: int) -> torch.Tensor:
     """Gated attention of a segment at positions pos0.. over the cached prefix ([hf]:656-701 under
     the block-causal rule): q/k norm + RoPE, the segment's K/V written into the cache at pos0..,
-    block-causal attention against cache rows 0..pos0+T-1, sigmoid gate, o_proj."""
+    block-causal attention against cache rows 0..pos0+T-1, sigmoid gate; returns (o_proj, its input)."""
     B, T, _ = x.shape
     hd = att.head_dim
     qg, kp, vp = _proj_many((att.q_proj, att.k_proj, att.v_proj), x)
@@ -330,7 +394,7 @@ def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: i
     cache.v[i][:, pos0:pos0 + T] = vp.view(B, T, -1, hd)
     o = attention.block_causal_attention(q, cache.k[i][:, :pos0 + T], cache.v[i][:, :pos0 + T], block=cache.block,
                                          q_offset=pos0, scale=float(att.scaling))
-    return _proj(att.o_proj, o.reshape(B, T, -1) * torch.sigmoid(gate))
+    return att.o_proj, o.reshape(B, T, -1) * torch.sigmoid(gate)
 
 
 @torch.no_grad()
@@ -350,24 +414,24 @@ def forward_segment(text_model, lm_head, cache: PrefixCache, ids: torch.Tensor, 
     if P + T > cache.capacity:
         raise ValueError(f"segment at {P}..{P + T} exceeds the cache capacity {cache.capacity}")
     h = text_model.embed_tokens(ids)
-    pending = None
+    pending = None  # (the last MLP's down_proj, its input): applied with the norm after it
     for i, kind in enumerate(cache.kinds):
         layer = text_model.layers[i]
         if pending is None:
             x = rmsnorm(h, layer.input_layernorm)
         else:
-            x, h = rmsnorm(pending, layer.input_layernorm, residual=h)
+            x, h = _proj_norm(*pending, layer.input_layernorm, h)
         if kind == LINEAR:
-            o = _gdn_segment(layer.linear_attn, x, cache, i, commit)
+            lin, a = _gdn_segment(layer.linear_attn, x, cache, i, commit)
         else:
-            o = _attention_segment(layer.self_attn, x, cache, i, P)
-        x, h = rmsnorm(o, layer.post_attention_layernorm, residual=h)
-        pending = _mlp(layer.mlp, x)
+            lin, a = _attention_segment(layer.self_attn, x, cache, i, P)
+        x, h = _proj_norm(lin, a, layer.post_attention_layernorm, h)
+        pending = _mlp_act(layer.mlp, x)
     if commit:
         cache.length = P + T
     if not logits:
-        return None
-    return _proj(lm_head, rmsnorm(pending, text_model.norm, residual=h)[0])
+        return None  # the cache is complete; the last MLP's down projection feeds only the logits
+    return _proj(lm_head, _proj_norm(*pending, text_model.norm, h)[0])
 
 
 @torch.no_grad()

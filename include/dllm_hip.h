@@ -267,6 +267,22 @@ int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const v
                                  const int* Ns, void* workspace, int workgroups, int swiglu, int dtype, void* stream);
 
 /*
+ * A projection followed by the residual add and RMSNorm of the next module, as the decoder layer
+ * runs them after o_proj / out_proj and after down_proj ([hf]:778-792; the post-attention norm,
+ * the next layer's input norm, the final norm): s = round(x W^T) + residual rounded to bf16 (written
+ * to sum_out) and y = s * rsqrt(mean(s^2) + eps) * (1 + w) (unit_offset = 1; 0: w as is), equal
+ * element for element to dllm_decode_linear_fwd followed by dllm_rmsnorm_fwd(.., residual,
+ * sum_out, ..), with the fixup launch of the first and the separate norm folded into one row-wise
+ * launch. x [M, K], W [N, K], residual / sum_out / y [M, N] bf16; norm weight [N] bf16 or fp32
+ * (dtype_w); N a multiple of 512 up to 8192; workgroups from dllm_decode_linear_workgroups(M, N,
+ * K); workspace of dllm_decode_linear_workspace_bytes(M, N, workgroups, 1) bytes (the pieces, then
+ * the projection's rounded whole tiles). All pointers 16-byte aligned.
+ */
+int dllm_decode_linear_rmsnorm_fwd(const void* x, const void* weight, void* workspace, int M, int N, int K,
+                                   int workgroups, const void* residual, void* sum_out, const void* norm_weight,
+                                   void* y, float eps, int unit_offset, int dtype, int dtype_w, void* stream);
+
+/*
  * Qwen3.5 RMSNorm over the last dim of x [rows, dim]: y = x * rsqrt(mean(x^2) + eps) * (1 + w)
  * in fp32 (unit_offset = 1; 0 applies w as is), rounded once to x's dtype.
  * Replaces [hf]:720-737 Qwen3_5RMSNorm as called by the decoder layer and the final norm

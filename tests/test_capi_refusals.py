@@ -91,6 +91,11 @@ def multi(x=P, M=32, K=128, count=1, Ns=(128,), ws=P, wgs=4, swiglu=0, dtype=BF,
             swiglu, dtype, None)
 
 
+def linrms(x=P, M=32, N=512, K=128, wgs=4, r=P, so=P, nw=P, y=P, dtype=BF, dtype_w=BF, ws=P):
+    """dllm_decode_linear_rmsnorm_fwd (the projection, then the residual add and RMSNorm)."""
+    return ("dllm_decode_linear_rmsnorm_fwd", x, P, ws, M, N, K, wgs, r, so, nw, y, 1e-6, 1, dtype, dtype_w, None)
+
+
 CASES = {
     # chunked gated delta rule (src/dllm_qwen38/gdn.py:48-123)
     "chunk null pointer": (chunk(q=None), EINVAL, "gdn: null pointer"),
@@ -201,6 +206,16 @@ CASES = {
     "linear misaligned workspace": (multi(ws=P2), EINVAL, "workspace must be a 16-byte aligned"),
     "linear too many workgroups": (multi(M=64, K=64 * 1024, Ns=(128 * 1024,), wgs=40000), EINVAL,
                                    "40000 workgroups (at most 32768)"),
+    "linear rmsnorm no residual": (linrms(r=None), EINVAL, "decode linear rmsnorm: null pointer"),
+    "linear rmsnorm no output": (linrms(y=None), EINVAL, "decode linear rmsnorm: null pointer"),
+    "linear rmsnorm fp16 weight": (linrms(dtype_w=2), EUNSUP, "norm weight dtype 2"),
+    "linear rmsnorm N % 512": (linrms(N=640), EUNSUP, "N=640 is not a multiple of 512"),
+    "linear rmsnorm N past 8192": (linrms(N=8704), EUNSUP, "N=8704 is not a multiple of 512 up to 8192"),
+    "linear rmsnorm misaligned sum": (linrms(so=P2), EINVAL, "must be 16-byte aligned"),
+    "linear rmsnorm 65 rows": (linrms(M=65), EUNSUP, "M=65 > 64 rows"),
+    "linear rmsnorm fp32": (linrms(dtype=F32), EUNSUP, "bf16 only"),
+    "linear rmsnorm K % 64": (linrms(K=96), EUNSUP, "K=96 is not a multiple of 64"),
+    "linear rmsnorm misaligned workspace": (linrms(ws=P2), EINVAL, "workspace must be a 16-byte aligned"),
     "noalloc bad sizes": (("dllm_decode_linear_fwd_noalloc", P, P, P, 0, 128, 128, 4, BF, None), EINVAL, "bad sizes"),
     "noalloc K % 64": (("dllm_decode_linear_fwd_noalloc", P, P, P, 32, 128, 100, 4, BF, None), EUNSUP,
                        "K=100 is not a multiple of 64"),
@@ -235,3 +250,18 @@ def test_empty_inputs_are_accepted_without_a_launch():
     assert L.dllm_gated_rmsnorm_fwd(P, P, P, P, 0, 64, 1e-6, BF, BF, None) == 0
     assert L.dllm_swiglu_fwd(P, P, P, 0, BF, None) == 0
     assert L.dllm_swiglu_rows_fwd(P, P, 8, P, 0, 8, BF, None) == 0
+
+
+@pytest.mark.parametrize("N", range(512, 9216, 512))
+def test_fused_norm_widths_agree_with_the_python_gate(N):
+    """dllm_decode_linear_rmsnorm_fwd takes exactly the row widths decode._norm_width_fused admits
+    (the forward then never sends it a width it refuses): an admitted width gets past the width
+    checks and is refused later, on K = 96."""
+    from dllm_qwen38_amd import decode
+
+    call = linrms(N=N, K=96)
+    rc = getattr(_lib.lib(), call[0])(*call[1:])
+    if decode._norm_width_fused(N):
+        assert rc == EUNSUP and "K=96 is not a multiple of 64" in _lib.last_error(), (N, _lib.last_error())
+    else:
+        assert rc == EUNSUP and "decode linear rmsnorm: N=" in _lib.last_error(), (N, _lib.last_error())

@@ -211,6 +211,60 @@ def test_decode_linear_multi_and_swiglu_epilogue(dev):
     assert (err <= 2 ** -6 * ref.abs() + 2 ** -10 * ref.abs().max()).all()
 
 
+@pytest.mark.parametrize("M,N,K,G,wdtype,unit", [
+    (32, 5120, 6144, None, torch.bfloat16, 1),   # o_proj / out_proj of the 27B-class decoder step
+    (32, 5120, 17408, None, torch.float32, 1),   # down_proj, fp32 norm weight
+    (1, 512, 64, 1, torch.bfloat16, 0),          # one row, one unit, w applied as is
+    (40, 1024, 1024, 7, torch.bfloat16, 1),      # two row tiles, seven workgroups
+    (64, 2048, 512, 191, torch.float32, 0),
+    (33, 3072, 256, 4096, torch.bfloat16, 1),    # more workgroups than units: one unit each
+    (17, 4096, 2048, None, torch.bfloat16, 1),
+    (32, 8192, 256, None, torch.bfloat16, 1),    # the widest row: two feature slots per thread
+])
+def test_decode_linear_rmsnorm_equals_projection_then_norm(dev, M, N, K, G, wdtype, unit):
+    """The fused projection + residual add + RMSNorm equals the projection (main and fixup launches,
+    same workgroup count) followed by the row RMSNorm with the residual, bit for bit in both the
+    normed output and the sum; the sum stays within the projection's bound of x W^T + r; a repeat
+    gives the same bits."""
+    from dllm_qwen38_amd import _lib, norms
+
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    nw = (torch.randn(N, generator=g) * 0.1).to(wdtype)
+    L = _lib.lib()
+    G = G or L.dllm_decode_linear_workgroups(M, N, K)
+    xd, wd, rd, nwd = x.to(dev), w.to(dev), r.to(dev), nw.to(dev)
+    eps = 1e-6
+    print(f"decode linear rmsnorm M={M} N={N} K={K} workgroups={G}", flush=True)
+
+    def fused():
+        s = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        work = decode._workspace(L, M, N, G, True, dev)
+        _lib.check(L.dllm_decode_linear_rmsnorm_fwd(
+            xd.data_ptr(), wd.data_ptr(), work.data_ptr(), M, N, K, G, rd.data_ptr(), s.data_ptr(), nwd.data_ptr(),
+            y.data_ptr(), eps, unit, _lib.DT_BF16, _lib.dtype_code(wdtype), _lib.stream_handle(dev)), "fused")
+        torch.cuda.synchronize()
+        return y.cpu(), s.cpu()
+
+    p = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    work = decode._workspace(L, M, 0, G, False, dev)
+    _lib.check(L.dllm_decode_linear_fwd(xd.data_ptr(), wd.data_ptr(), p.data_ptr(), work.data_ptr(), M, N, K, G,
+                                        _lib.DT_BF16, _lib.stream_handle(dev)), "projection")
+    y_ref, s_ref = norms.rmsnorm(p, nwd, eps, residual=rd, unit_offset=bool(unit))
+    torch.cuda.synchronize()
+    y, s = fused()
+    assert torch.equal(s, s_ref.cpu()), "sum differs from projection + residual"
+    assert torch.equal(y, y_ref.cpu()), "normed output differs from the row RMSNorm"
+    ref = x.float() @ w.float().T
+    bound = 2 ** -8 * ref.abs() + 2 ** -16 * (x.float().abs() @ w.float().abs().T) + 2 ** -8 * (ref + r.float()).abs()
+    assert ((s.float() - (ref + r.float())).abs() <= bound + 2 ** -8 * r.float().abs()).all()
+    y2, s2 = fused()
+    assert torch.equal(y, y2) and torch.equal(s, s2)
+
+
 @pytest.fixture(scope="module")
 def tiny(dev):
     cpu_model, cpu_head = tiny_hf_model(seed=0)

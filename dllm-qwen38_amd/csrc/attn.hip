@@ -57,7 +57,8 @@ struct AttnArgs {
   const void* cosb;  // [L, rd] rotary tables in the activation dtype
   const void* sinb;
   int rd;
-  // gate non-null: out = attention * sigmoid(gate), gate [B, 2L, Hq, d] with these strides
+  // gate non-null: out = attention * sigmoid(gate), gate [B, 2L, Hq, d] (block-causal mode:
+  // [B, M, Hq, d]) with these strides
   const void* gate;
   long long g_sb;
   int g_st, g_sh;
@@ -886,12 +887,11 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
     bf16* op = (bf16*)a.out + (orow * a.Hq + hq) * a.d;
     // the output gate (gated attention, [hf]:698): bf16(bf16(o) * bf16(sigmoid(gate))), the
     // rounding of the separate elementwise product
-    bool gated = false;
-    if constexpr (!BC) gated = a.gate != nullptr;
-    if (gated) {
+    if (a.gate) {
       // every gate value of the row first (in flight together), then the products;
       // sigmoid(x) = 1 / (1 + 2^(-x log2 e)) from the hardware exp2 and reciprocal, rounded to bf16
-      const bf16* gp = (const bf16*)a.gate + b * a.g_sb + (long long)(qh * L + qi) * a.g_st + (long long)hq * a.g_sh;
+      const bf16* gp = (const bf16*)a.gate + b * a.g_sb + (long long)(BC ? qi : qh * L + qi) * a.g_st +
+                       (long long)hq * a.g_sh;
       bf16x4 g4[DT][4];
 #pragma unroll
       for (int t = 0; t < DT; ++t)
@@ -926,11 +926,13 @@ __global__ __launch_bounds__(512) void bd_attn_sp_kernel(AttnArgs a) {
 }
 
 // Merge of the key shares of a split block-causal launch: per (b, query, head) row, with
-// M = max_s m_s and w_s = 2^(m_s - M), out = (sum_s w_s O_s) / (sum_s w_s l_s). One thread per
-// four consecutive d.
+// M = max_s m_s and w_s = 2^(m_s - M), out = (sum_s w_s O_s) / (sum_s w_s l_s), times sigmoid(gate)
+// with the main kernel's rounding when a gate is given (row (b, i, h) of [B, M, Hq, d] at
+// b g_sb + i g_st + h g_sh). One thread per four consecutive d.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ opart,
                                                            const float* __restrict__ mlpart, bf16* __restrict__ out,
-                                                           long long rows, int d, int ks) {
+                                                           long long rows, int d, int ks, const bf16* __restrict__ gate,
+                                                           long long g_sb, int g_st, int g_sh, int M, int Hq) {
   const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
   const int q4 = d / 4;
   if (t >= rows * q4) return;
@@ -949,8 +951,20 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   }
   const float inv = 1.f / l;
   bf16x4 r;
+  if (gate) {
+    const long long bi = row / Hq;  // b M + i
+    const bf16x4 g4 = *(const bf16x4*)(gate + (bi / M) * g_sb + (long long)(bi % M) * g_st +
+                                       (long long)(row % Hq) * g_sh + c);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = (bf16)(o[i] * inv);
+    for (int i = 0; i < 4; ++i) {
+      const float ov = (float)(bf16)(o[i] * inv);
+      const float sg = (float)(bf16)__builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * (float)g4[i]));
+      r[i] = (bf16)(ov * sg);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (bf16)(o[i] * inv);
+  }
   *(bf16x4*)(out + row * d + c) = r;
 }
 
@@ -972,8 +986,8 @@ static int launch_attn_sp(const AttnArgs& a, hipStream_t st) {
   if (ks > 1) {
     const long long rows = (long long)a.B * a.M * a.Hq;
     const long long n = rows * (D / 4);
-    attn_combine_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(a.opart, a.mlpart, (bf16*)a.out,
-                                                                                rows, D, ks);
+    attn_combine_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(
+        a.opart, a.mlpart, (bf16*)a.out, rows, D, ks, (const bf16*)a.gate, a.g_sb, a.g_st, a.g_sh, a.M, a.Hq);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(DLLM_ELAUNCH, "attention combine launch: %s", hipGetErrorString(e));
   }
@@ -984,7 +998,7 @@ static bool fits32(long long x) { return x >= -2147483647LL && x <= 2147483647LL
 
 // shared by both entry points: vectorisation check and kernel choice
 template <bool BC>
-static int dispatch_attn(AttnArgs& a, const int64_t* const sts[3], int dtype, hipStream_t st) {
+static int dispatch_attn(AttnArgs& a, const int64_t* const sts[3], int dtype, hipStream_t st, bool direct_only = false) {
   const int d = a.d;
   const int esz = dtype == DT_BF16 ? 2 : 4;
   const int vel = 16 / esz;
@@ -1004,6 +1018,9 @@ static int dispatch_attn(AttnArgs& a, const int64_t* const sts[3], int dtype, hi
         default: return launch_attn_sp<256, BC>(a, st);
       }
     }
+    if (direct_only)
+      return fail(DLLM_EUNSUPPORTED, "attention: the gated form needs the direct-load kernel (bf16, d in {64, 128, "
+                                     "256}, 16-byte aligned rows of exactly d elements, a positive scale)");
     switch (dw) {
       case 32: return launch_attn<32, true, BC>(a, st);
       case 64: return launch_attn<64, true, BC>(a, st);
@@ -1011,6 +1028,7 @@ static int dispatch_attn(AttnArgs& a, const int64_t* const sts[3], int dtype, hi
       default: return launch_attn<256, true, BC>(a, st);
     }
   }
+  if (direct_only) return fail(DLLM_EUNSUPPORTED, "attention: the gated form is bf16 only");
   if (dtype == DT_F32) {
     switch (dw) {
       case 32: return launch_attn<32, false, BC>(a, st);
@@ -1127,11 +1145,11 @@ extern "C" int dllm_bd_attention_gated_fwd(const void* q, const int64_t* q_strid
   }
 }
 
-extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, const void* k,
-                                               const int64_t* k_strides, const void* v, const int64_t* v_strides,
-                                               void* out, int B, int M, int N, int q0, int Hq, int Hkv, int d,
-                                               int block, float scale, int dtype, float* workspace, int key_splits,
-                                               void* stream) {
+static int block_causal_attention(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                  const void* v, const int64_t* v_strides, const void* gate,
+                                  const int64_t* gate_strides, void* out, int B, int M, int N, int q0, int Hq, int Hkv,
+                                  int d, int block, float scale, int dtype, float* workspace, int key_splits,
+                                  void* stream) {
   if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides)
     return fail(DLLM_EINVAL, "block-causal attention: null pointer");
   if (B <= 0 || M <= 0 || N <= 0 || q0 < 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || block <= 0)
@@ -1149,6 +1167,9 @@ extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_s
     if (!fits32((long long)rows[i] * sts[i][1]) || !fits32((long long)H[i] * sts[i][2]) ||
         !fits32((long long)rows[i] * sts[i][1] + (long long)H[i] * sts[i][2]))
       return fail(DLLM_EUNSUPPORTED, "attention: per-sequence extent exceeds 32-bit element offsets");
+  if (gate && (!fits32((long long)M * gate_strides[1] + (long long)Hq * gate_strides[2]) || gate_strides[1] % 4 ||
+               gate_strides[2] % 4 || gate_strides[0] % 4 || (uintptr_t)gate % 8))
+    return fail(DLLM_EUNSUPPORTED, "block-causal attention: gate rows must be 8-byte aligned with 32-bit extents");
   AttnArgs a = {};
   a.q = q; a.k = k; a.v = v; a.out = out;
   fill_strides(a, q_strides, k_strides, v_strides);
@@ -1158,5 +1179,31 @@ extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_s
   a.opart = workspace;
   a.mlpart = workspace ? workspace + (long long)key_splits * B * M * Hq * d : nullptr;
   a.scale_log2e = scale * 1.4426950408889634f;
-  return dispatch_attn<true>(a, sts, dtype, (hipStream_t)stream);
+  a.gate = gate;
+  if (gate) {
+    a.g_sb = gate_strides[0];
+    a.g_st = (int)gate_strides[1];
+    a.g_sh = (int)gate_strides[2];
+  }
+  return dispatch_attn<true>(a, sts, dtype, (hipStream_t)stream, gate != nullptr);
+}
+
+extern "C" int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, const void* k,
+                                               const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                               void* out, int B, int M, int N, int q0, int Hq, int Hkv, int d,
+                                               int block, float scale, int dtype, float* workspace, int key_splits,
+                                               void* stream) {
+  return block_causal_attention(q, q_strides, k, k_strides, v, v_strides, nullptr, nullptr, out, B, M, N, q0, Hq, Hkv,
+                                d, block, scale, dtype, workspace, key_splits, stream);
+}
+
+extern "C" int dllm_block_causal_attention_gated_fwd(const void* q, const int64_t* q_strides, const void* k,
+                                                     const int64_t* k_strides, const void* v,
+                                                     const int64_t* v_strides, const void* gate,
+                                                     const int64_t* gate_strides, void* out, int B, int M, int N,
+                                                     int q0, int Hq, int Hkv, int d, int block, float scale,
+                                                     int dtype, float* workspace, int key_splits, void* stream) {
+  if (!gate || !gate_strides) return fail(DLLM_EINVAL, "block-causal attention: null gate");
+  return block_causal_attention(q, q_strides, k, k_strides, v, v_strides, gate, gate_strides, out, B, M, N, q0, Hq,
+                                Hkv, d, block, scale, dtype, workspace, key_splits, stream);
 }

@@ -90,6 +90,9 @@ _SIGNATURES = {
     "dllm_block_causal_attention_fwd": (_c_int, [
         _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_void_p, _c_int, _c_void_p]),
+    "dllm_block_causal_attention_gated_fwd": (_c_int, [
+        _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int,
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_void_p, _c_int, _c_void_p]),
 }
 
 _LIB = None

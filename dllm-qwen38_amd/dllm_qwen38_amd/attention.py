@@ -132,9 +132,18 @@ def _key_splits(q: torch.Tensor, M: int, N: int, d: int) -> int:
     return max(1, min(32, -(-N // 256)))
 
 
+def block_causal_gate_fused(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether block_causal_attention takes a gate for these q [B, M, Hq, d] and k/v [B, N, Hkv, d]:
+    the direct-load kernel's inputs (bf16, d in {64, 128, 256}, 16-byte aligned rows)."""
+    d = q.shape[-1]
+    return (q.dtype == torch.bfloat16 and d in (64, 128, 256)
+            and all(t.dtype == q.dtype and t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+                    and all(t.stride(i) % 8 == 0 for i in range(3)) for t in (q, k, v)))
+
+
 def block_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block: int, q_offset: int = 0,
                            scale: float | None = None, out: torch.Tensor | None = None,
-                           key_splits: int | None = None) -> torch.Tensor:
+                           key_splits: int | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
     """Block-causal attention of a query segment against a key/value cache (the clean-prefix cache
     of the cached decoder; the reference re-runs the whole forward instead, decode.py:63-66).
 
@@ -142,7 +151,9 @@ def block_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     0..N-1 (token-major, any batch/token/head strides, last dim contiguous; rotary already applied).
     Query i sees key j iff j // block <= (q_offset + i) // block (blockdiff.py:43-47 with the query
     rows offset). Returns [B, M, Hq, d]. key_splits (default: chosen for a decoding step's few query
-    rows) spreads the key tiles over several workgroups whose partial results are merged."""
+    rows) spreads the key tiles over several workgroups whose partial results are merged. gate
+    [B, M, Hq, d] (any batch/token/head strides, last dim contiguous; bf16, the direct-load kernel's
+    head sizes): the output is attention * sigmoid(gate) ([hf]:698), applied at the output store."""
     dev = _lib.require_device(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q must be [B, M, Hq, d] and k, v [B, N, Hkv, d]")
@@ -166,6 +177,14 @@ def block_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     sc = d ** -0.5 if scale is None else float(scale)
     ks = _key_splits(q, M, N, d) if key_splits is None else int(key_splits)
     work = torch.empty(ks * B * M * Hq * (d + 2), dtype=torch.float32, device=dev) if ks > 1 else None
+    if gate is not None:
+        if tuple(gate.shape) != (B, M, Hq, d) or gate.dtype != q.dtype or gate.stride(-1) != 1:
+            raise ValueError("gate must be [B, M, Hq, d] of q's dtype with a contiguous last dim")
+        _lib.check(_lib.lib().dllm_block_causal_attention_gated_fwd(
+            q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
+            gate.data_ptr(), _lib.strides3(gate), out.data_ptr(), B, M, N, q_offset, Hq, Hkv, d, block, sc,
+            _lib.dtype_code(q.dtype), _lib.ptr(work), ks, _lib.stream_handle(dev)), "dllm_block_causal_attention_gated_fwd")
+        return out
     _lib.check(_lib.lib().dllm_block_causal_attention_fwd(
         q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), v.data_ptr(), _lib.strides3(v),
         out.data_ptr(), B, M, N, q_offset, Hq, Hkv, d, block, sc, _lib.dtype_code(q.dtype), _lib.ptr(work), ks,

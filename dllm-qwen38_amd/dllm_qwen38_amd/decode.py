@@ -170,10 +170,11 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | 
     return y.reshape(*x.shape[:-1], N)
 
 
-def decode_linear_multi(x: torch.Tensor, weights: list, *, swiglu: bool = False):
+def decode_linear_multi(x: torch.Tensor, weights: list, *, swiglu: bool = False, outs: list | None = None):
     """Up to four projections of the same x [..., K] in one launch (their weights [N_i, K] bf16).
     Returns the list of [..., N_i] outputs, or with swiglu (gate, up) the MLP activation
-    round(round(silu(x gate^T)) * (x up^T)) as one tensor."""
+    round(round(silu(x gate^T)) * (x up^T)) as one tensor. outs (without swiglu): per projection
+    None or a contiguous bf16 tensor of M x N_i elements to write it into (a cache's rows)."""
     dev = _lib.require_device(x, *weights)
     K = x.shape[-1]
     if not 1 <= len(weights) <= 4:
@@ -190,7 +191,17 @@ def decode_linear_multi(x: torch.Tensor, weights: list, *, swiglu: bool = False)
     G = _workgroups(L, M, sum(-(-n // 128) * 128 for n in Ns), K)
     if G <= 0:
         raise ValueError(f"decode_linear_multi does not take M={M} K={K} (M <= 64, K % 64 == 0)")
-    outs = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in (Ns[:1] if swiglu else Ns)]
+    given = outs
+    if given is not None and (swiglu or len(given) != len(Ns)):
+        raise ValueError("outs takes one entry per projection, without swiglu")
+    outs = []
+    for i, n in enumerate(Ns[:1] if swiglu else Ns):
+        o = given[i] if given is not None else None
+        if o is None:
+            o = torch.empty(M, n, dtype=torch.bfloat16, device=dev)
+        elif o.numel() != M * n or o.dtype != torch.bfloat16 or not o.is_contiguous() or o.device != dev:
+            raise ValueError(f"outs[{i}] must be a contiguous bf16 tensor of {M} x {n} elements on {dev}")
+        outs.append(o)
     if swiglu:
         outs.append(outs[0])  # not written
     work = _workspace(L, M, Ns[0], G, swiglu, dev)
@@ -385,16 +396,29 @@ def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: i
     block-causal attention against cache rows 0..pos0+T-1, sigmoid gate; returns (o_proj, its input)."""
     B, T, _ = x.shape
     hd = att.head_dim
-    qg, kp, vp = _proj_many((att.q_proj, att.k_proj, att.v_proj), x)
+    kc, vc = cache.k[i][:, pos0:pos0 + T], cache.v[i][:, pos0:pos0 + T]
+    # one sequence: the segment's cache rows are contiguous, and the projections and the k prologue
+    # write into them directly
+    direct = B == 1 and kc.is_contiguous() and vc.is_contiguous()
+    lins = (att.q_proj, att.k_proj, att.v_proj)
+    if direct and _fast(lins, x):
+        qg, kp, _ = decode_linear_multi(x, [lin.weight for lin in lins], outs=[None, None, vc])
+    else:
+        qg, kp, vp = _proj_many(lins, x)
+        vc.copy_(vp.view(B, T, -1, hd))
     q, gate = torch.chunk(qg.view(B, T, -1, 2 * hd), 2, dim=-1)
-    gate = gate.reshape(B, T, -1)
     cos, sin = cache.cos[pos0:pos0 + T], cache.sin[pos0:pos0 + T]
-    q, k = norms.qk_norm_rope(q, kp.view(B, T, -1, hd), att.q_norm, att.k_norm, cos, sin, T)
-    cache.k[i][:, pos0:pos0 + T] = k
-    cache.v[i][:, pos0:pos0 + T] = vp.view(B, T, -1, hd)
-    o = attention.block_causal_attention(q, cache.k[i][:, :pos0 + T], cache.v[i][:, :pos0 + T], block=cache.block,
-                                         q_offset=pos0, scale=float(att.scaling))
-    return att.o_proj, o.reshape(B, T, -1) * torch.sigmoid(gate)
+    q, k = norms.qk_norm_rope(q, kp.view(B, T, -1, hd), att.q_norm, att.k_norm, cos, sin, T,
+                              k_out=kc if direct else None)
+    if not direct:
+        kc.copy_(k)
+    kv = (cache.k[i][:, :pos0 + T], cache.v[i][:, :pos0 + T])
+    if attention.block_causal_gate_fused(q, *kv):
+        o = attention.block_causal_attention(q, *kv, block=cache.block, q_offset=pos0, scale=float(att.scaling),
+                                             gate=gate)
+        return att.o_proj, o.reshape(B, T, -1)
+    o = attention.block_causal_attention(q, *kv, block=cache.block, q_offset=pos0, scale=float(att.scaling))
+    return att.o_proj, o.reshape(B, T, -1) * torch.sigmoid(gate.reshape(B, T, -1))
 
 
 @torch.no_grad()

@@ -86,10 +86,12 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_norm, k_norm, cos: torch.Tensor, sin: torch.Tensor, L: int):
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_norm, k_norm, cos: torch.Tensor, sin: torch.Tensor, L: int, *,
+                 k_out: torch.Tensor | None = None):
     """q [B, S, Hq, hd], k [B, S, Hkv, hd] (any batch/token/head strides, last dim contiguous) ->
     contiguous normed-and-rotated copies. cos/sin [L, rotary_dim] in the activation dtype; token t
-    uses row t mod L."""
+    uses row t mod L. k_out: a contiguous [B, S, Hkv, hd] tensor to write the k result into (a
+    key cache's rows)."""
     dev = _lib.require_device(q, k, cos, sin)
     B, S, Hq, hd = q.shape
     Hkv = k.shape[2]
@@ -99,7 +101,12 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_norm, k_norm, cos: torch.Te
     cs, sn = _c(cos.to(q.dtype)), _c(sin.to(q.dtype))
     wq, wk = _c(q_norm.weight), _c(k_norm.weight)
     qo = torch.empty(B, S, Hq, hd, dtype=q.dtype, device=dev)
-    ko = torch.empty(B, S, Hkv, hd, dtype=k.dtype, device=dev)
+    if k_out is None:
+        ko = torch.empty(B, S, Hkv, hd, dtype=k.dtype, device=dev)
+    elif tuple(k_out.shape) != (B, S, Hkv, hd) or k_out.dtype != k.dtype or not k_out.is_contiguous():
+        raise ValueError(f"k_out must be a contiguous {(B, S, Hkv, hd)} tensor of k's dtype")
+    else:
+        ko = k_out
     _lib.check(_lib.lib().dllm_qk_norm_rope_fwd(
         q.data_ptr(), _lib.strides3(q), k.data_ptr(), _lib.strides3(k), wq.data_ptr(), wk.data_ptr(),
         cs.data_ptr(), sn.data_ptr(), qo.data_ptr(), ko.data_ptr(), B, S, L, Hq, Hkv, hd, rd, _eps(q_norm),

@@ -225,6 +225,21 @@ int dllm_block_causal_attention_fwd(const void* q, const int64_t* q_strides, con
                                     int key_splits, void* stream);
 
 /*
+ * The same with the gated attention layer's output gate ([hf]:698, o * sigmoid(gate) before o_proj,
+ * as the cached decoder's attention layer runs it) applied at the output store or the merge of the
+ * key shares: out = bf16(bf16(attention) * bf16(sigmoid(gate))), the rounding of the separate
+ * elementwise product. gate [B,M,Hq,d] bf16 with strides {b,t,h} in elements (multiples of 4,
+ * 8-byte aligned rows; the gate half of the q_proj output read in place). Takes the direct-load
+ * kernel's shapes only (bf16, d in {64,128,256}, 16-byte aligned q/k/v rows, positive scale);
+ * others return -2.
+ */
+int dllm_block_causal_attention_gated_fwd(const void* q, const int64_t* q_strides, const void* k,
+                                          const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                          const void* gate, const int64_t* gate_strides, void* out, int B, int M,
+                                          int N, int q0, int Hq, int Hkv, int d, int block, float scale, int dtype,
+                                          float* workspace, int key_splits, void* stream);
+
+/*
  * Projections of a decoding step (few token rows): y[M,N] = x[M,K] W[N,K]^T, bf16 in and out, fp32
  * accumulation; M <= 64, K a multiple of 64, x and W row-major and 16-byte aligned, y [M,N]
  * contiguous. Replaces the nn.Linear calls (in_proj_*, q/k/v/o_proj, the MLP, lm_head) that every

@@ -216,6 +216,18 @@ CASES = {
     "linear rmsnorm fp32": (linrms(dtype=F32), EUNSUP, "bf16 only"),
     "linear rmsnorm K % 64": (linrms(K=96), EUNSUP, "K=96 is not a multiple of 64"),
     "linear rmsnorm misaligned workspace": (linrms(ws=P2), EINVAL, "workspace must be a 16-byte aligned"),
+    "bc gated null gate": (("dllm_block_causal_attention_gated_fwd", P, s3(8, 8, 8), P, s3(8, 8, 8), P, s3(8, 8, 8),
+                            None, None, P, 1, 32, 64, 32, 4, 2, 64, 32, 0.125, BF, None, 1, None), EINVAL,
+                           "null gate"),
+    "bc gated fp32": (("dllm_block_causal_attention_gated_fwd", P, s3(8, 8, 8), P, s3(8, 8, 8), P, s3(8, 8, 8),
+                       P, s3(8, 8, 8), P, 1, 32, 64, 32, 4, 2, 64, 32, 0.125, F32, None, 1, None), EUNSUP,
+                      "gated form is bf16 only"),
+    "bc gated misaligned gate": (("dllm_block_causal_attention_gated_fwd", P, s3(8, 8, 8), P, s3(8, 8, 8), P,
+                                  s3(8, 8, 8), P + 4, s3(8, 8, 8), P, 1, 32, 64, 32, 4, 2, 64, 32, 0.125, BF, None, 1,
+                                  None), EUNSUP, "gate rows must be 8-byte aligned"),
+    "bc gated d 80": (("dllm_block_causal_attention_gated_fwd", P, s3(8, 8, 8), P, s3(8, 8, 8), P, s3(8, 8, 8),
+                       P, s3(8, 8, 8), P, 1, 32, 64, 32, 4, 2, 80, 32, 0.125, BF, None, 1, None), EUNSUP,
+                      "needs the direct-load kernel"),
     "noalloc bad sizes": (("dllm_decode_linear_fwd_noalloc", P, P, P, 0, 128, 128, 4, BF, None), EINVAL, "bad sizes"),
     "noalloc K % 64": (("dllm_decode_linear_fwd_noalloc", P, P, P, 32, 128, 100, 4, BF, None), EUNSUP,
                        "K=100 is not a multiple of 64"),

@@ -89,6 +89,31 @@ def test_key_split_attention_matches_oracle(dev, ks):
     _check_att(one, ref, torch.bfloat16, vmax, "unsplit")
 
 
+@pytest.mark.parametrize("ks", [1, 4])
+@pytest.mark.parametrize("B,M,N,q0,Hq,Hkv,d", [
+    (1, 32, 1024, 992, 6, 2, 256),   # a decoding step of the 27B-class heads
+    (2, 20, 100, 80, 4, 2, 128),     # ragged rows, two sequences
+    (1, 64, 600, 536, 8, 2, 64),
+])
+def test_block_causal_gate_equals_the_separate_product(dev, ks, B, M, N, q0, Hq, Hkv, d):
+    """The output gate fused into the block-causal attention (at the output store, or at the merge
+    of the key shares) against the separate bf16 product o * sigmoid(gate) on the same attention
+    output: within one bf16 rounding of sigmoid (hardware exp2 / reciprocal vs torch's), 2^-7 |ref|;
+    the gate read in place as the second half of each head's 2d columns, as the decoder slices it."""
+    q, k, v = (t.to(dev) for t in _att_inputs(B, M, N, Hq, Hkv, d, torch.bfloat16, seed=M + N + d + ks))
+    g = torch.Generator().manual_seed(ks * 1000 + d)
+    qg = (torch.randn(B, M, Hq, 2 * d, generator=g) * 2).to(torch.bfloat16).to(dev)
+    gate = qg[..., d:]
+    assert attention.block_causal_gate_fused(q, k, v)
+    got = attention.block_causal_attention(q, k, v, block=32, q_offset=q0, key_splits=ks, gate=gate)
+    o = attention.block_causal_attention(q, k, v, block=32, q_offset=q0, key_splits=ks)
+    ref = (o * torch.sigmoid(gate)).float()
+    torch.cuda.synchronize()
+    err = (got.float() - ref).abs()
+    print(f"gated ks={ks} B={B} M={M} d={d}: max|d|={err.max().item():.3e}")
+    assert (err <= 2 ** -7 * ref.abs() + 1e-6).all()
+
+
 def test_27b_class_decoding_step_attention(dev):
     """24 query / 4 key-value heads of dim 256, 4096 cached keys, one block of 32 queries."""
     q, k, v = _att_inputs(1, 32, 4096, 24, 4, 256, torch.bfloat16, seed=27)

@@ -236,6 +236,174 @@ __global__ __launch_bounds__(256) void decode_linear_fixup_kernel(LinArgs a, Lin
     if (n + i < sg.N) y[n + i] = (bf16)s[i];
 }
 
+// The Gated DeltaNet layer's input projections (in_proj_qkv | in_proj_z | in_proj_b | in_proj_a)
+// of a decoding step, finished together with the short conv and the gates that read them.
+struct GdnPrologue {
+  const bf16* prefix;  // [sequences, C, P]: the conv carry-in (the prefix's last P projections), or null
+  const void* conv_w;  // [C, width]
+  const void* conv_b;  // [C] or null
+  bf16* mixed;         // [M, C]: conv + SiLU of the qkv projection
+  const void* a_log;   // [H]
+  const void* dt_bias;  // [H]
+  float* beta;         // [M, H]
+  float* g;            // [M, H]
+  int T;               // tokens per sequence (divides 32): row m is token m % T of sequence m / T
+  int width, P;        // conv width; carry-in length (0 or width - 1)
+};
+
+// One block per output tile (32 rows x 128 features): the tile's rounded values (stored whole by
+// the streaming kernel, or its pieces summed in workgroup order and stored, as the fixup does; all
+// of a thread's loads go out before their sums) go to LDS, then by projection:
+//   qkv: the causal depthwise conv + SiLU (width KW) of every (row, channel) of the tile, as the
+//        generic conv kernel computes it: taps in order from the oldest, inputs rounded through the
+//        weight type, the sum and the SiLU rounded. A thread walks a run of up to 16 rows of one
+//        channel inside one sequence (a tile holds whole sequences) with the last KW - 1 inputs in
+//        registers: before the run they are the tile's earlier rows or, at a sequence's start, the
+//        carry-in, loaded (with the channel's weights) before the tile's values;
+//   z:   nothing more (whole tiles take no block work at all);
+//   b:   beta = round(sigmoid(b)), a:   g = -exp(A_log) softplus(a + dt_bias), as the gates kernel,
+//        each thread one head column (its A_log and dt_bias loaded before the tile's values).
+template <typename TW, typename TP, int KW>
+__global__ __launch_bounds__(256) void decode_gdn_prologue_kernel(LinArgs a, GdnPrologue p) {
+  static_assert(KW >= 2 && KW <= 8, "conv width");
+  __shared__ float vals[32][129];
+  const int tile = blockIdx.x;
+  const int mt = tile / a.ntn, nt = tile - mt * a.ntn;
+  const int si = lin_seg(a, nt);
+  const LinSeg& sg = a.seg[si];
+  const int n0 = (nt - sg.tile0) * 128;
+  const int t0 = tile * a.ns;
+  const int w0 = lin_owner(a, t0), w1 = lin_owner(a, t0 + a.ns - 1);
+  const bool split = w0 != w1;
+  if (si == 1 && !split) return;
+  const int cl0 = threadIdx.x & 127;
+  // conv runs: item = run * 128 + channel, run j covering tile rows [j rl, (j + 1) rl); this thread
+  // takes items tid, tid + 256, ..
+  const int rl = p.T < 16 ? p.T : 16;  // rows per run
+  const int nitems = 128 * (32 / rl);
+  float wv[KW], pre[KW - 1], bv = 0.f;
+  auto run_rows = [&](int item, int& row0, int& pos0) {
+    row0 = (item >> 7) * rl;
+    pos0 = (mt * 32 + row0) % p.T;
+  };
+  auto load_pre = [&](int item, float* h) {  // carry-in of the run's sequence (its first run only)
+    int row0, pos0;
+    run_rows(item, row0, pos0);
+    const long long seq = (mt * 32 + row0) / p.T;
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j) {
+      const int u = pos0 - (KW - 1) + j;  // position of tap j before the run's first row
+      h[j] = (u < 0 && p.P) ? round_through<TW>((float)p.prefix[(seq * sg.N + n0 + (item & 127)) * p.P + (p.P + u)])
+                            : 0.f;
+    }
+  };
+  if (si == 0 && n0 + cl0 < sg.N) {
+    const TW* const w = (const TW*)p.conv_w + (long long)(n0 + cl0) * KW;
+#pragma unroll
+    for (int j = 0; j < KW; ++j) wv[j] = to_f32(w[j]);
+    bv = p.conv_b ? to_f32(((const TW*)p.conv_b)[n0 + cl0]) : 0.f;
+    if ((int)threadIdx.x < nitems) load_pre(threadIdx.x, pre);
+  }
+  // gates: the head column n0 + cl0 of this thread
+  float dtb = 0.f, nea = 0.f;
+  if (si == 3 && n0 + cl0 < sg.N) {
+    dtb = to_f32(((const TP*)p.dt_bias)[n0 + cl0]);
+    nea = -expf(to_f32(((const TP*)p.a_log)[n0 + cl0]));
+  }
+  constexpr int KQ = LIN_TILE / 4 / 256;  // float4 slots per thread: q = k 256 + tid, row q / 32, features 4 (q % 32) ..
+  if (split) {
+    constexpr int T4 = LIN_TILE / 4;
+    const f32x4* const pp = (const f32x4*)a.part + threadIdx.x;
+    const long long first = (long long)(2 * w0 + (lin_start(a, w0) >= t0 ? 0 : 1)) * T4;
+    f32x4 sum[KQ];
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) sum[k] = pp[first + 256 * k];
+    for (int wb = w0 + 1; wb <= w1; wb += 4) {
+      f32x4 pc[4][KQ];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (wb + i <= w1)
+#pragma unroll
+          for (int k = 0; k < KQ; ++k) pc[i][k] = pp[(long long)(2 * (wb + i)) * T4 + 256 * k];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (wb + i <= w1)
+#pragma unroll
+          for (int k = 0; k < KQ; ++k) sum[k] += pc[i][k];
+    }
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+      const int q = k * 256 + threadIdx.x;
+      const int r = q >> 5, c = (q & 31) * 4;
+      const int m = mt * 32 + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = round_through<bf16>(sum[k][e]);
+        vals[r][c + e] = v;
+        if (m < a.M && n0 + c + e < sg.N) sg.y[(long long)m * sg.N + n0 + c + e] = (bf16)v;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+      const int q = k * 256 + threadIdx.x;
+      const int r = q >> 5, c = (q & 31) * 4;
+      const int m = mt * 32 + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        vals[r][c + e] = (m < a.M && n0 + c + e < sg.N) ? (float)sg.y[(long long)m * sg.N + n0 + c + e] : 0.f;
+    }
+  }
+  if (si == 1) return;
+  __syncthreads();
+  if (si == 0) {
+    for (int item = threadIdx.x; item < nitems; item += 256) {
+      const int cl = item & 127;
+      const int n = n0 + cl;
+      int row0, pos0;
+      run_rows(item, row0, pos0);
+      if (n >= sg.N || mt * 32 + row0 >= a.M) continue;
+      float h[KW - 1];
+      if (item != (int)threadIdx.x) load_pre(item, h);
+      else
+#pragma unroll
+        for (int j = 0; j < KW - 1; ++j) h[j] = pre[j];
+#pragma unroll
+      for (int j = 0; j < KW - 1; ++j) {  // taps inside the sequence before the run: the tile's rows
+        const int u = pos0 - (KW - 1) + j;
+        if (u >= 0) h[j] = round_through<TW>(vals[row0 - (KW - 1) + j][cl]);
+      }
+      bf16* const out = p.mixed + (long long)(mt * 32 + row0) * sg.N + n;
+      for (int t = 0; t < rl; ++t) {
+        if (mt * 32 + row0 + t >= a.M) break;
+        const float xv = round_through<TW>(vals[row0 + t][cl]);
+        float acc = bv;
+#pragma unroll
+        for (int j = 0; j < KW - 1; ++j) acc = __builtin_fmaf(wv[j], h[j], acc);
+        acc = __builtin_fmaf(wv[KW - 1], xv, acc);
+#pragma unroll
+        for (int j = 0; j + 1 < KW - 1; ++j) h[j] = h[j + 1];
+        h[KW - 2] = xv;
+        acc = round_through<TW>(acc);
+        out[(long long)t * sg.N] = (bf16)round_through<TW>(silu_f32(acc));
+      }
+    }
+  } else if (n0 + cl0 < sg.N) {
+    for (int r = threadIdx.x >> 7; r < 32; r += 2) {
+      const int m = mt * 32 + r;
+      if (m >= a.M) break;
+      const float x = vals[r][cl0];
+      if (si == 2) {
+        p.beta[(long long)m * sg.N + n0 + cl0] = round_through<bf16>(1.f / (1.f + expf(-x)));
+      } else {
+        const float av = x + dtb;
+        const float sp = av > 20.f ? av : log1pf(expf(av));
+        p.g[(long long)m * sg.N + n0 + cl0] = nea * sp;
+      }
+    }
+  }
+}
+
 // SwiGLU epilogue over every gate tile, block (tile, c) for chunk c: y0 = round(round(silu(gate)) *
 // up), gate and up each the rounded sum of their tile (stored whole by the main kernel, or summed
 // here from the pieces).
@@ -516,6 +684,60 @@ extern "C" int dllm_decode_linear_rmsnorm_fwd(const void* x, const void* weight,
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "decode linear rmsnorm launch: %s", hipGetErrorString(e));
+  return DLLM_OK;
+}
+
+extern "C" int dllm_decode_gdn_prologue_fwd(const void* x, int M, int K, const void* const* weights, void* const* outs,
+                                            const int* Ns, void* workspace, int workgroups, int T,
+                                            const void* conv_prefix, int prefix_len, const void* conv_w,
+                                            const void* conv_b, int width, void* mixed, const void* a_log,
+                                            const void* dt_bias, float* beta, float* g, int dtype,
+                                            int dtype_conv, int dtype_param, void* stream) {
+  if (!weights || !outs || !Ns || !conv_w || !mixed || !a_log || !dt_bias || !beta || !g)
+    return fail(DLLM_EINVAL, "gdn prologue: null pointer");
+  if (T <= 0 || 32 % T || M <= 0 || M % T)
+    return fail(DLLM_EUNSUPPORTED, "gdn prologue: T=%d must divide 32 and M=%d", T, M);
+  if (width < 2 || width > 4) return fail(DLLM_EUNSUPPORTED, "gdn prologue: conv width %d (2..4)", width);
+  if (!(prefix_len == 0 || prefix_len == width - 1) || (prefix_len > 0 && !conv_prefix))
+    return fail(DLLM_EINVAL, "gdn prologue: carry-in of %d positions (0 or width - 1 = %d, with a pointer)",
+                prefix_len, width - 1);
+  if (Ns[2] != Ns[3]) return fail(DLLM_EINVAL, "gdn prologue: b and a of %d and %d heads", Ns[2], Ns[3]);
+  if (dtype_conv != DT_BF16 && dtype_conv != DT_F32)
+    return fail(DLLM_EUNSUPPORTED, "gdn prologue: conv weight dtype %d", dtype_conv);
+  if (dtype_param != DT_BF16 && dtype_param != DT_F32)
+    return fail(DLLM_EUNSUPPORTED, "gdn prologue: A_log / dt_bias dtype %d", dtype_param);
+  LinArgs a;
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = lin_launch_main(x, M, K, 4, weights, outs, Ns, workspace, workgroups, 0, dtype, st, a);
+  if (rc != DLLM_OK) return rc;
+  GdnPrologue p;
+  p.prefix = prefix_len > 0 ? (const bf16*)conv_prefix : nullptr;
+  p.conv_w = conv_w;
+  p.conv_b = conv_b;
+  p.mixed = (bf16*)mixed;
+  p.a_log = a_log;
+  p.dt_bias = dt_bias;
+  p.beta = beta;
+  p.g = g;
+  p.T = T;
+  p.width = width;
+  p.P = prefix_len;
+  const dim3 grid((unsigned)(a.ntn * ((M + 31) / 32)));
+  auto go = [&](auto tw, auto tp) {
+    using TW = decltype(tw);
+    using TP = decltype(tp);
+    switch (width) {
+      case 2: decode_gdn_prologue_kernel<TW, TP, 2><<<grid, 256, 0, st>>>(a, p); break;
+      case 3: decode_gdn_prologue_kernel<TW, TP, 3><<<grid, 256, 0, st>>>(a, p); break;
+      default: decode_gdn_prologue_kernel<TW, TP, 4><<<grid, 256, 0, st>>>(a, p); break;
+    }
+  };
+  if (dtype_conv == DT_BF16 && dtype_param == DT_F32) go(bf16{}, float{});
+  else if (dtype_conv == DT_BF16) go(bf16{}, bf16{});
+  else if (dtype_param == DT_F32) go(float{}, float{});
+  else go(float{}, bf16{});
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DLLM_ELAUNCH, "gdn prologue launch: %s", hipGetErrorString(e));
   return DLLM_OK;
 }
 

@@ -85,6 +85,10 @@ _SIGNATURES = {
     "dllm_decode_linear_rmsnorm_fwd": (_c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
         _c_float, _c_int, _c_int, _c_int, _c_void_p]),
+    "dllm_decode_gdn_prologue_fwd": (_c_int, [
+        _c_void_p, _c_int, _c_int, _c_voidpp, _c_voidpp, _c_intp, _c_void_p, _c_int, _c_int, _c_void_p, _c_int,
+        _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+        _c_void_p]),
     "dllm_gdn_gates_fwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int,
                                     _c_int, _c_int, _c_void_p]),
     "dllm_block_causal_attention_fwd": (_c_int, [

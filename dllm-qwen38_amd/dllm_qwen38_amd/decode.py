@@ -282,6 +282,63 @@ def _proj(lin, x: torch.Tensor) -> torch.Tensor:
     return lin(x)
 
 
+def decode_gdn_prologue(m, x: torch.Tensor, conv_prefix: torch.Tensor | None, T: int):
+    """The Gated DeltaNet mixer `m`'s input projections of a decoding segment with the short conv
+    and the gates (reference gdn.py:212-226 with conv_prefix): x [..., K] bf16, rows = sequences of T
+    tokens (T dividing 32, at most 64 rows), conv_prefix [sequences, conv_dim, width - 1] (the
+    prefix's last projections) or None (zeros). Returns (raw, mixed, z, beta, g): the qkv projection
+    and its conv + SiLU [..., conv_dim], z [..., value_dim], beta and g [..., H] fp32, equal element
+    for element to the projections, `gdn._beta_g` and `gdn.causal_conv1d_fn` run separately; one
+    streaming launch and one launch for the rest."""
+    lins = (m.in_proj_qkv, m.in_proj_z, m.in_proj_b, m.in_proj_a)
+    dev = _lib.require_device(x, *[lin.weight for lin in lins])
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    ws = [lin.weight.contiguous() for lin in lins]
+    Ns = [w.shape[0] for w in ws]
+    C, H = Ns[0], Ns[2]
+    cw = m.conv1d.weight.reshape(C, -1).contiguous()
+    width = cw.shape[1]
+    cb = None if m.conv1d.bias is None else m.conv1d.bias.contiguous()
+    if conv_prefix is not None and (tuple(conv_prefix.shape) != (M // T, C, width - 1) or
+                                    conv_prefix.dtype != torch.bfloat16 or not conv_prefix.is_contiguous()):
+        raise ValueError(f"conv_prefix must be a contiguous bf16 [{M // T}, {C}, {width - 1}] tensor")
+    L = _lib.lib()
+    G = _workgroups(L, M, sum(-(-n // 128) * 128 for n in Ns), K)
+    if G <= 0:
+        raise ValueError(f"decode_gdn_prologue does not take M={M} K={K} (M <= 64, K % 64 == 0)")
+    outs = [torch.empty(M, n, dtype=torch.bfloat16, device=dev) for n in Ns]
+    mixed = torch.empty(M, C, dtype=torch.bfloat16, device=dev)
+    beta = torch.empty(M, H, dtype=torch.float32, device=dev)
+    g = torch.empty(M, H, dtype=torch.float32, device=dev)
+    al = m.A_log.reshape(H).contiguous()
+    db = m.dt_bias.reshape(H).to(al.dtype).contiguous()
+    work = _workspace(L, M, Ns[0], G, False, dev)
+    warr = (ctypes.c_void_p * 4)(*[w.data_ptr() for w in ws])
+    oarr = (ctypes.c_void_p * 4)(*[o.data_ptr() for o in outs])
+    narr = (ctypes.c_int * 4)(*Ns)
+    _lib.check(L.dllm_decode_gdn_prologue_fwd(
+        x2.data_ptr(), M, K, warr, oarr, narr, work.data_ptr(), G, T, _lib.ptr(conv_prefix),
+        0 if conv_prefix is None else width - 1, cw.data_ptr(), _lib.ptr(cb), width, mixed.data_ptr(),
+        al.data_ptr(), db.data_ptr(), beta.data_ptr(), g.data_ptr(), _lib.DT_BF16, _lib.dtype_code(cw.dtype),
+        _lib.dtype_code(al.dtype), _lib.stream_handle(dev)), "dllm_decode_gdn_prologue_fwd")
+    lead = x.shape[:-1]
+    return (outs[0].reshape(*lead, C), mixed.reshape(*lead, C), outs[1].reshape(*lead, Ns[1]),
+            beta.reshape(*lead, H), g.reshape(*lead, H))
+
+
+def _prologue_fused(m, x: torch.Tensor, conv_prefix, T: int) -> bool:
+    """Whether `decode_gdn_prologue` takes this mixer and segment."""
+    lins = (m.in_proj_qkv, m.in_proj_z, m.in_proj_b, m.in_proj_a)
+    w = m.conv1d.weight
+    return (_fast(lins, x) and 32 % T == 0 and m.activation in ("silu", "swish") and 2 <= w.shape[-1] <= 4
+            and w.dtype in (torch.bfloat16, torch.float32) and m.A_log.dtype in (torch.bfloat16, torch.float32)
+            and m.in_proj_b.out_features == m.in_proj_a.out_features
+            and (conv_prefix is None or (conv_prefix.dtype == torch.bfloat16 and conv_prefix.is_contiguous()
+                                         and conv_prefix.shape[-1] == w.shape[-1] - 1)))
+
+
 def _norm_width_fused(N: int) -> bool:
     """Whether dllm_decode_linear_rmsnorm_fwd takes rows of N features: N a multiple of 512 up to
     8192 whose 512-feature vectors split over at most 8 waves with at most 8 vectors per lane (the
@@ -371,10 +428,13 @@ def _gdn_segment(m, x: torch.Tensor, cache: PrefixCache, i: int, commit: bool) -
     prefix's last projections in, the recurrence starts from the prefix state; with commit, the
     state after the segment and its last projections replace the cached ones."""
     B, T, _ = x.shape
-    raw, z, bp, ap = _proj_many((m.in_proj_qkv, m.in_proj_z, m.in_proj_b, m.in_proj_a), x)  # raw [B, T, conv_dim]
-    beta, g = gdn._beta_g(m, bp, ap)
-    mixed = gdn.causal_conv1d_fn(raw.transpose(1, 2), m.conv1d.weight.squeeze(1), m.conv1d.bias,
-                                 activation=m.activation, conv_prefix=cache.conv[i]).transpose(1, 2)
+    if _prologue_fused(m, x, cache.conv[i], T):
+        raw, mixed, z, beta, g = decode_gdn_prologue(m, x, cache.conv[i], T)  # raw, mixed [B, T, conv_dim]
+    else:
+        raw, z, bp, ap = _proj_many((m.in_proj_qkv, m.in_proj_z, m.in_proj_b, m.in_proj_a), x)
+        beta, g = gdn._beta_g(m, bp, ap)
+        mixed = gdn.causal_conv1d_fn(raw.transpose(1, 2), m.conv1d.weight.squeeze(1), m.conv1d.bias,
+                                     activation=m.activation, conv_prefix=cache.conv[i]).transpose(1, 2)
     q, k, v = gdn._split_qkv(mixed, m, B, T)
     core, states = gdn._core(q, k, v, g, beta, chunk_size=cache.block, initial_state=cache.state[i],
                              need_states=commit)

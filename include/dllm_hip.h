@@ -282,6 +282,26 @@ int dllm_decode_linear_multi_fwd(const void* x, int M, int K, int count, const v
                                  const int* Ns, void* workspace, int workgroups, int swiglu, int dtype, void* stream);
 
 /*
+ * The Gated DeltaNet mixer's input projections of a decoding step finished together with what reads
+ * them next (src/dllm_qwen38/gdn.py:212-226 with conv_prefix, as the cached decoder runs it):
+ * weights[0..3] = in_proj_qkv [C, K], in_proj_z, in_proj_b [H, K], in_proj_a [H, K] into
+ * outs[0..3] [M, Ns[i]] (bf16, contiguous), one launch as dllm_decode_linear_multi_fwd (same
+ * workgroups and workspace), then one launch that sums the split tiles and forms
+ * mixed [M, C] = SiLU(causal depthwise conv of the qkv projection, width 2..4), the history
+ * before each sequence's first token taken from conv_prefix [M/T, C, width-1] (prefix_len =
+ * width - 1; prefix_len = 0: zeros), beta [M, H] = sigmoid(b) rounded to bf16 and
+ * g [M, H] = -exp(A_log) softplus(a + dt_bias) (fp32). Rows are M/T sequences of T tokens, T
+ * dividing 32. Element for element the results of dllm_decode_linear_multi_fwd,
+ * dllm_causal_conv1d_fwd (activation on) and dllm_gdn_gates_fwd run separately. conv_w [C, width]
+ * and conv_b [C] (nullable) in dtype_conv, A_log and dt_bias [H] in dtype_param (bf16 or fp32).
+ */
+int dllm_decode_gdn_prologue_fwd(const void* x, int M, int K, const void* const* weights, void* const* outs,
+                                 const int* Ns, void* workspace, int workgroups, int T, const void* conv_prefix,
+                                 int prefix_len, const void* conv_w, const void* conv_b, int width, void* mixed,
+                                 const void* a_log, const void* dt_bias, float* beta, float* g, int dtype,
+                                 int dtype_conv, int dtype_param, void* stream);
+
+/*
  * A projection followed by the residual add and RMSNorm of the next module, as the decoder layer
  * runs them after o_proj / out_proj and after down_proj ([hf]:778-792; the post-attention norm,
  * the next layer's input norm, the final norm): s = round(x W^T) + residual rounded to bf16 (written

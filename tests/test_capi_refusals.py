@@ -96,6 +96,13 @@ def linrms(x=P, M=32, N=512, K=128, wgs=4, r=P, so=P, nw=P, y=P, dtype=BF, dtype
     return ("dllm_decode_linear_rmsnorm_fwd", x, P, ws, M, N, K, wgs, r, so, nw, y, 1e-6, 1, dtype, dtype_w, None)
 
 
+def prologue(M=32, T=32, Ns=(768, 512, 16, 16), prefix=P, plen=3, width=4, dconv=BF, dparam=F32, mixed=P, K=96):
+    """dllm_decode_gdn_prologue_fwd (in_proj_qkv | z | b | a, then the conv and the gates); K = 96 makes
+    an argument set that passes the prologue's own checks fail in the projection's."""
+    return ("dllm_decode_gdn_prologue_fwd", P, M, K, ptrs(P, P, P, P), ptrs(P, P, P, P), ints(*Ns), P, 4, T, prefix,
+            plen, P, None, width, mixed, P, P, P, P, BF, dconv, dparam, None)
+
+
 CASES = {
     # chunked gated delta rule (src/dllm_qwen38/gdn.py:48-123)
     "chunk null pointer": (chunk(q=None), EINVAL, "gdn: null pointer"),
@@ -228,6 +235,16 @@ CASES = {
     "bc gated d 80": (("dllm_block_causal_attention_gated_fwd", P, s3(8, 8, 8), P, s3(8, 8, 8), P, s3(8, 8, 8),
                        P, s3(8, 8, 8), P, 1, 32, 64, 32, 4, 2, 80, 32, 0.125, BF, None, 1, None), EUNSUP,
                       "needs the direct-load kernel"),
+    "prologue no mixed output": (prologue(mixed=None), EINVAL, "gdn prologue: null pointer"),
+    "prologue T 24": (prologue(T=24), EUNSUP, "T=24 must divide 32"),
+    "prologue M not whole sequences": (prologue(M=40, T=16), EUNSUP, "T=16 must divide 32 and M=40"),
+    "prologue width 9": (prologue(width=9, plen=8), EUNSUP, "conv width 9"),
+    "prologue carry-in length": (prologue(plen=2), EINVAL, "carry-in of 2 positions"),
+    "prologue carry-in pointer": (prologue(prefix=None), EINVAL, "carry-in of 3 positions"),
+    "prologue b and a differ": (prologue(Ns=(768, 512, 16, 32)), EINVAL, "b and a of 16 and 32 heads"),
+    "prologue conv fp16": (prologue(dconv=2), EUNSUP, "conv weight dtype 2"),
+    "prologue param fp16": (prologue(dparam=2), EUNSUP, "A_log / dt_bias dtype 2"),
+    "prologue projection checks": (prologue(), EUNSUP, "K=96 is not a multiple of 64"),
     "noalloc bad sizes": (("dllm_decode_linear_fwd_noalloc", P, P, P, 0, 128, 128, 4, BF, None), EINVAL, "bad sizes"),
     "noalloc K % 64": (("dllm_decode_linear_fwd_noalloc", P, P, P, 32, 128, 100, 4, BF, None), EUNSUP,
                        "K=100 is not a multiple of 64"),

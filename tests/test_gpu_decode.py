@@ -290,6 +290,63 @@ def test_decode_linear_rmsnorm_equals_projection_then_norm(dev, M, N, K, G, wdty
     assert torch.equal(y, y2) and torch.equal(s, s2)
 
 
+class _Mixer(torch.nn.Module):
+    """The attributes of a Gated DeltaNet mixer that the decoding-step prologue reads, seeded."""
+
+    def __init__(self, K, C, Nz, H, width, conv_bias, wdtype, pdtype, seed, dev):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+
+        def lin(n):
+            m = torch.nn.Linear(K, n, bias=False)
+            m.weight.data = (torch.randn(n, K, generator=g) * 0.03).to(torch.bfloat16)
+            return m
+
+        self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a = lin(C), lin(Nz), lin(H), lin(H)
+        self.conv1d = torch.nn.Conv1d(C, C, width, groups=C, bias=conv_bias, padding=width - 1)
+        self.conv1d.weight.data = (torch.rand(C, 1, width, generator=g) - 0.5).to(wdtype)
+        if conv_bias:
+            self.conv1d.bias.data = (torch.rand(C, generator=g) - 0.5).to(wdtype)
+        self.A_log = torch.nn.Parameter(torch.log(torch.rand(H, generator=g) * 15 + 1).to(pdtype))
+        self.dt_bias = torch.nn.Parameter(torch.randn(H, generator=g).to(pdtype))
+        self.activation = "silu"
+        self.to(dev)
+
+
+@pytest.mark.parametrize("M,T,K,C,Nz,H,width,bias,prefix,wdtype,pdtype", [
+    (32, 32, 1024, 768, 512, 16, 4, False, True, torch.bfloat16, torch.float32),   # every tile split
+    (32, 32, 64, 768, 512, 16, 4, False, True, torch.bfloat16, torch.float32),     # one unit per tile: none split
+    (64, 32, 512, 1024, 256, 48, 4, True, False, torch.float32, torch.bfloat16),   # two sequences, no carry-in
+    (64, 16, 768, 640, 384, 130, 3, True, True, torch.bfloat16, torch.bfloat16),   # four sequences of 16; 130 heads
+    (8, 8, 256, 300, 200, 7, 4, False, True, torch.bfloat16, torch.float32),       # ragged widths, tile rows past M
+])
+def test_decode_gdn_prologue_equals_the_separate_kernels(dev, M, T, K, C, Nz, H, width, bias, prefix, wdtype,
+                                                           pdtype):
+    """The GDN mixer's input projections finished with the short conv (and its carry-in) and the
+    gates in one launch equal the projections, the conv kernel and the gates kernel run separately,
+    bit for bit: the projections, z, the conv + SiLU output, beta and g."""
+    from dllm_qwen38_amd import gdn, norms
+
+    m = _Mixer(K, C, Nz, H, width, bias, wdtype, pdtype, seed=M + K + C, dev=dev)
+    g = torch.Generator().manual_seed(M * T + C)
+    B = M // T
+    x = torch.randn(B, T, K, generator=g).to(torch.bfloat16).to(dev)
+    pre = (torch.randn(B, C, width - 1, generator=g).to(torch.bfloat16).to(dev) if prefix else None)
+    print(f"gdn prologue M={M} T={T} K={K} C={C} H={H} width={width}", flush=True)
+    assert decode._prologue_fused(m, x, pre, T)
+    raw, mixed, z, beta, gg = decode.decode_gdn_prologue(m, x, pre, T)
+    lins = (m.in_proj_qkv, m.in_proj_z, m.in_proj_b, m.in_proj_a)
+    raw_r, z_r, b_r, a_r = decode.decode_linear_multi(x, [lin.weight for lin in lins])
+    beta_r, g_r = norms.gdn_gates(b_r, a_r, m.A_log, m.dt_bias)
+    mixed_r = gdn.causal_conv1d_fn(raw_r.transpose(1, 2), m.conv1d.weight.squeeze(1), m.conv1d.bias,
+                                   activation="silu", conv_prefix=pre).transpose(1, 2)
+    torch.cuda.synchronize()
+    for name, got, ref in (("raw", raw, raw_r), ("z", z, z_r), ("mixed", mixed, mixed_r), ("beta", beta, beta_r),
+                           ("g", gg, g_r)):
+        assert got.shape == ref.shape, name
+        assert torch.equal(got, ref), f"{name} differs: max|d|={(got.float() - ref.float()).abs().max().item():.3e}"
+
+
 @pytest.fixture(scope="module")
 def tiny(dev):
     cpu_model, cpu_head = tiny_hf_model(seed=0)

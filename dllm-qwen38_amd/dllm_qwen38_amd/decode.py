@@ -112,6 +112,13 @@ def generate(text_model, lm_head, prompt_ids: list[int], *, n_blocks: int, block
     return trace
 
 
+# False: forward_segment runs each bit-exact fused decoding-step launch (projection end + norm, the
+# GDN in_proj end, the attention layer's direct cache writes) as the separate launches it replaces,
+# whose results it equals bit for bit; for comparisons and measurement. (The attention output gate
+# inside the attention kernel rounds its sigmoid from the hardware exponential, within one bf16
+# rounding of torch's, and is not switched.)
+FUSED = True
+
 _WORKSPACES: dict = {}
 _SIZES: dict = {}
 
@@ -356,7 +363,7 @@ def _proj_norm(lin, a: torch.Tensor, norm, h: torch.Tensor):
     (`decode_linear_rmsnorm`), else the projection and the norm kernel."""
     w = lin.weight
     rows = a.numel() // a.shape[-1]
-    if (lin.bias is None and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and h.dtype == torch.bfloat16
+    if (FUSED and lin.bias is None and a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and h.dtype == torch.bfloat16
             and rows <= 64 and w.shape[1] % 64 == 0 and _norm_width_fused(w.shape[0])
             and norm.weight.dtype in (torch.bfloat16, torch.float32)):
         return decode_linear_rmsnorm(a, w, h, norm.weight, _eps(norm))
@@ -428,7 +435,7 @@ def _gdn_segment(m, x: torch.Tensor, cache: PrefixCache, i: int, commit: bool) -
     prefix's last projections in, the recurrence starts from the prefix state; with commit, the
     state after the segment and its last projections replace the cached ones."""
     B, T, _ = x.shape
-    if _prologue_fused(m, x, cache.conv[i], T):
+    if FUSED and _prologue_fused(m, x, cache.conv[i], T):
         raw, mixed, z, beta, g = decode_gdn_prologue(m, x, cache.conv[i], T)  # raw, mixed [B, T, conv_dim]
     else:
         raw, z, bp, ap = _proj_many((m.in_proj_qkv, m.in_proj_z, m.in_proj_b, m.in_proj_a), x)
@@ -459,7 +466,7 @@ def _attention_segment(att, x: torch.Tensor, cache: PrefixCache, i: int, pos0: i
     kc, vc = cache.k[i][:, pos0:pos0 + T], cache.v[i][:, pos0:pos0 + T]
     # one sequence: the segment's cache rows are contiguous, and the projections and the k prologue
     # write into them directly
-    direct = B == 1 and kc.is_contiguous() and vc.is_contiguous()
+    direct = FUSED and B == 1 and kc.is_contiguous() and vc.is_contiguous()
     lins = (att.q_proj, att.k_proj, att.v_proj)
     if direct and _fast(lins, x):
         qg, kp, _ = decode_linear_multi(x, [lin.weight for lin in lins], outs=[None, None, vc])

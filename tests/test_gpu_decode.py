@@ -422,6 +422,40 @@ def stack27(dev):
     return hybrid.build(c, device=dev, dtype=torch.bfloat16, seed=21)
 
 
+def test_27b_class_fused_step_equals_the_separate_launches(stack27, dev):
+    """A cached denoising step and a commit on 27B-class layers (GDN and attention) with the fused
+    decoding-step launches (projection end + residual norm, the GDN in_proj end with conv and gates,
+    the attention layer's direct cache writes) against the same forward with each of them as the
+    separate launches it replaces: logits, GDN states, conv carry-in and K/V cache bit-equal."""
+    model, lm_head = stack27
+    block, P = 32, 256
+    g = torch.Generator().manual_seed(12)
+    x0 = torch.randint(0, 151936, (1, P + 2 * block), generator=g).to(dev)
+    xt = x0.clone()
+    xt[:, P + 7:] = 151935
+    runs = {}
+    try:
+        for fused in (True, False):
+            decode.FUSED = fused
+            cache = decode.PrefixCache(model, batch=1, capacity=P + 2 * block, block=block)
+            decode.forward_segment(model, lm_head, cache, x0[:, :P], commit=True, logits=False)
+            step = decode.forward_segment(model, lm_head, cache, xt[:, P:P + block], commit=False)
+            decode.forward_segment(model, lm_head, cache, x0[:, P:P + block], commit=True, logits=False)
+            step2 = decode.forward_segment(model, lm_head, cache, xt[:, P + block:], commit=False)
+            torch.cuda.synchronize()
+            runs[fused] = (step, step2, cache)
+    finally:
+        decode.FUSED = True
+    (a1, a2, ca), (b1, b2, cb) = runs[True], runs[False]
+    assert torch.equal(a1, b1) and torch.equal(a2, b2), "logits differ"
+    for i in ca.state:
+        if ca.state[i] is not None:
+            assert torch.equal(ca.state[i], cb.state[i]) and torch.equal(ca.conv[i], cb.conv[i]), f"layer {i} GDN cache"
+    for i in ca.k:
+        n = P + block
+        assert torch.equal(ca.k[i][:, :n], cb.k[i][:, :n]) and torch.equal(ca.v[i][:, :n], cb.v[i][:, :n]), f"layer {i} K/V"
+
+
 def test_27b_class_cached_step_matches_the_forward_bf16(stack27, dev):
     model, lm_head = stack27
     block, P = 32, 512

@@ -30,7 +30,11 @@
 //     launch: the feature tiles run through the weights in turn. With the SwiGLU epilogue
 //     (gate | up) the second kernel writes round(round(silu(gate)) * up), the MLP's activation,
 //     over the whole gate projection (whole tiles were stored rounded, the up tiles in the
-//     workspace).
+//     workspace);
+//   * the second kernel can also finish what reads the projection next, from the same sums: the
+//     residual add and RMSNorm after out_proj / o_proj / down_proj (one workgroup per token row)
+//     or, after a Gated DeltaNet layer's four input projections, the short conv and the gates (one
+//     block per tile). Either equals the separate launches bit for bit.
 #include <algorithm>
 #include <mutex>
 

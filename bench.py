@@ -205,10 +205,12 @@ GDN_WORKLOADS = {
 
 
 def bench_gdn_layer(a):
-    """One step = one state-fork GDN layer call: the conv of both streams and the fused fork. With
-    pieces > 1 the step is StateForkPlan.run_overlapped (the conv of each block range beside the
-    fork of the range before; bit-identical results). The per-kernel roofline comes from a second
-    pass of the two kernels back to back, each between HIP events."""
+    """One step = one state-fork GDN layer call: the conv of both streams and the fused fork (with
+    the v channels' conv inside the fork where that measured faster: the conv launch then covers
+    the q and k channels; bit-identical results). With pieces > 1 the step is
+    StateForkPlan.run_overlapped (the conv of each block range beside the fork of the range before;
+    bit-identical results). The per-kernel roofline comes from a second pass of the two kernels back
+    to back, each between HIP events."""
     import torch
 
     from dllm_qwen38_amd import gdn, inputs
@@ -267,10 +269,13 @@ def bench_gdn_layer(a):
     core_avg = sum(core_ms) / len(core_ms)
     conv_avg = sum(conv_ms) / len(conv_ms)
 
-    # the fork kernel's algorithmic bytes: conv outputs of both streams read once, beta and g of
-    # both streams (fp32), both outputs, the fp32 state snapshots
+    # the fork kernel's algorithmic bytes: the q/k/v rows of both streams read once (with the v conv
+    # inside the fork, the v rows are the conv's inputs: the same bytes), beta and g of both streams
+    # (fp32), both outputs, the fp32 state snapshots, and with the v conv the v channels' conv tails
     Cd, T = s.conv_dim, s.B * s.L
     core_bytes = (2 * T * Cd * 2 + 2 * T * s.Hv * 8 + 2 * T * s.Hv * s.D * 2 + (T // s.block) * s.Hv * s.D * s.D * 4)
+    if plan.vconv:
+        core_bytes += (T // s.block) * s.Hv * s.D * 3 * 2
     core_flops = gdn.layer_flops(s.B, s.L, s.Hv, s.D, s.D, s.block)
     achieved = core_bytes / (core_avg * 1e-3) / 1e9
     res = {
@@ -293,7 +298,7 @@ def bench_gdn_layer(a):
         "step_ms": _dist(per_step),
         "kernels_ms": {"conv_fork": conv_avg, "gdn_state_fork": core_avg,
                        "conv_fork_dist": _dist(conv_ms), "gdn_state_fork_dist": _dist(core_ms)},
-        "schedule": {"pieces": pieces, "ms_per_step_conv_then_fork": seq_step_ms},
+        "schedule": {"pieces": pieces, "vconv": plan.vconv, "ms_per_step_conv_then_fork": seq_step_ms},
         "layer_hbm": {"algorithmic_bytes": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block),
                       "step_gbs": gdn.layer_bytes(s.B, s.L, s.Hk, s.Hv, s.D, s.D, s.block) / (step_ms * 1e-3) / 1e9},
         "mfma": {"kernel": "gdn_state_fork", "algorithmic_tflops": core_flops / (core_avg * 1e-3) / 1e12,

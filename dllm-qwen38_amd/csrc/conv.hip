@@ -27,10 +27,10 @@ template <typename TX, typename TW, int K, int VEC, int BLK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BLK > 0 ? 5 : 1, BLK > 0 ? 5 : 8))) void conv_fork_kernel(
     const TX* __restrict__ raw0, const TX* __restrict__ rawt, const TW* __restrict__ w,
     const TW* __restrict__ bias, TX* __restrict__ y0, TX* __restrict__ yt, TX* __restrict__ tails,
-    int L, int Cd, int block, int cold_noised, int kb_off) {
+    int L, int Cd, int block, int cold_noised, int kb_off, int cy) {
   const int cg = blockIdx.x * blockDim.x + threadIdx.x;  // channel group
   const int c0 = cg * VEC;
-  if (c0 >= Cd) return;
+  if (c0 >= cy) return;  // channels [cy, Cd): not this launch's (their conv runs elsewhere)
   if (BLK > 0) block = BLK;
   const int kblk = blockIdx.y + kb_off;  // the launch covers blocks [kb_off, kb_off + gridDim.y)
   const int b = blockIdx.z;
@@ -169,10 +169,10 @@ __global__ __launch_bounds__(256) void conv_generic_kernel(
 template <typename TX, typename TW>
 static int launch_fork(const void* raw0, const void* rawt, const void* w, const void* bias, void* y0,
                        void* yt, void* tails, int B, int L, int Cd, int K, int block, int cold, int kb0,
-                       int nkb, hipStream_t st) {
+                       int nkb, int cy, hipStream_t st) {
   const int nb = nkb;  // blocks of this launch, from kb0
   constexpr int V = 16 / sizeof(TX);  // 16-byte row segments per thread
-  const bool vec_ok = (Cd % V == 0) && ((uintptr_t)raw0 % 16 == 0) && ((uintptr_t)rawt % 16 == 0) &&
+  const bool vec_ok = (Cd % V == 0) && (cy % V == 0) && ((uintptr_t)raw0 % 16 == 0) && ((uintptr_t)rawt % 16 == 0) &&
                       ((uintptr_t)y0 % 16 == 0) && ((uintptr_t)yt % 16 == 0) &&
                       ((uintptr_t)tails % 16 == 0);  // tails rows of VEC*(K-1) elements are 16-byte multiples
   bool done = false;
@@ -180,36 +180,36 @@ static int launch_fork(const void* raw0, const void* rawt, const void* w, const 
     if (K == 4 && vec_ok && block == 32) {
       // 8-byte channel groups at five resident waves per SIMD: at the 27B-class shape (B = 4,
       // L = 4096, conv_dim = 10240) the 20480 waves are exactly four rounds of the chip's slots
-      const int groups = Cd / 4;
+      const int groups = cy / 4;
       dim3 grid((groups + 255) / 256, nb, B);
       conv_fork_kernel<TX, TW, 4, 4, 32><<<grid, 256, 0, st>>>(
           (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-          Cd, block, cold, kb0);
+          Cd, block, cold, kb0, cy);
       done = true;
     }
   }
   if (done) {
   } else if (K == 4 && vec_ok) {
-    const int groups = Cd / V;
+    const int groups = cy / V;
     dim3 grid((groups + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 4, V, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold, kb0);
+        Cd, block, cold, kb0, cy);
   } else if (K == 4) {
-    dim3 grid((Cd + 255) / 256, nb, B);
+    dim3 grid((cy + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 4, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold, kb0);
+        Cd, block, cold, kb0, cy);
   } else if (K == 2) {
-    dim3 grid((Cd + 255) / 256, nb, B);
+    dim3 grid((cy + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 2, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold, kb0);
+        Cd, block, cold, kb0, cy);
   } else if (K == 3) {
-    dim3 grid((Cd + 255) / 256, nb, B);
+    dim3 grid((cy + 255) / 256, nb, B);
     conv_fork_kernel<TX, TW, 3, 1, 0><<<grid, 256, 0, st>>>(
         (const TX*)raw0, (const TX*)rawt, (const TW*)w, (const TW*)bias, (TX*)y0, (TX*)yt, (TX*)tails, L,
-        Cd, block, cold, kb0);
+        Cd, block, cold, kb0, cy);
   } else {
     return fail(DLLM_EUNSUPPORTED, "conv fork: kernel width %d not supported (2, 3 or 4)", K);
   }
@@ -225,7 +225,7 @@ using namespace dllm;
 // The fork conv over blocks [kb0, kb1) of every sequence.
 static int conv_fork(const void* raw0, const void* rawt, const void* weight, const void* bias, void* y0, void* yt,
                      void* tails, int B, int L, int conv_dim, int width, int block, int dtype_x, int dtype_w,
-                     int flags, int kb0, int kb1, hipStream_t st) {
+                     int flags, int kb0, int kb1, hipStream_t st, int y_channels = -1) {
   if (!raw0 || !rawt || !weight || !y0 || !yt) return fail(DLLM_EINVAL, "conv fork: null pointer");
   if (B <= 0 || L <= 0 || conv_dim <= 0 || block <= 0)
     return fail(DLLM_EINVAL, "conv fork: bad sizes B=%d L=%d conv_dim=%d block=%d", B, L, conv_dim, block);
@@ -234,14 +234,17 @@ static int conv_fork(const void* raw0, const void* rawt, const void* weight, con
   if (kb0 < 0 || kb1 > L / block || kb0 >= kb1)
     return fail(DLLM_EINVAL, "conv fork: block range [%d, %d) of %d", kb0, kb1, L / block);
   const int cold = flags & 1, n = kb1 - kb0;
+  const int cy = y_channels < 0 ? conv_dim : y_channels;
+  if (cy > conv_dim) return fail(DLLM_EINVAL, "conv fork: y_channels %d > conv_dim %d", cy, conv_dim);
+  if (cy == 0) return DLLM_OK;
   if (dtype_x == DT_BF16 && dtype_w == DT_BF16)
-    return launch_fork<bf16, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
+    return launch_fork<bf16, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, cy, st);
   if (dtype_x == DT_F32 && dtype_w == DT_F32)
-    return launch_fork<float, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
+    return launch_fork<float, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, cy, st);
   if (dtype_x == DT_BF16 && dtype_w == DT_F32)
-    return launch_fork<bf16, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
+    return launch_fork<bf16, float>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, cy, st);
   if (dtype_x == DT_F32 && dtype_w == DT_BF16)
-    return launch_fork<float, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, st);
+    return launch_fork<float, bf16>(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, cold, kb0, n, cy, st);
   return fail(DLLM_EUNSUPPORTED, "conv fork: dtype pair (%d, %d) not supported", dtype_x, dtype_w);
 }
 
@@ -251,6 +254,16 @@ extern "C" int dllm_conv_fork_fwd(const void* raw0, const void* rawt, const void
   const int nb = block > 0 && L > 0 && L % block == 0 ? L / block : 1;  // sizes are checked by conv_fork
   return conv_fork(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, dtype_x, dtype_w, flags, 0,
                    nb, (hipStream_t)stream);
+}
+
+extern "C" int dllm_conv_fork_channels_range_fwd(const void* raw0, const void* rawt, const void* weight,
+                                                 const void* bias, void* y0, void* yt, void* tails, int B, int L,
+                                                 int conv_dim, int width, int block, int dtype_x, int dtype_w,
+                                                 int flags, int block_begin, int block_end, int y_channels,
+                                                 void* stream) {
+  if (y_channels < 0) return fail(DLLM_EINVAL, "conv fork: y_channels %d < 0", y_channels);
+  return conv_fork(raw0, rawt, weight, bias, y0, yt, tails, B, L, conv_dim, width, block, dtype_x, dtype_w, flags,
+                   block_begin, block_end, (hipStream_t)stream, y_channels);
 }
 
 extern "C" int dllm_conv_fork_range_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,

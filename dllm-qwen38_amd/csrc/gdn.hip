@@ -62,6 +62,17 @@ struct GdnArgs {
   // from (the snapshot of the block before it, in the states layout; null: zeros)
   int t_rows, snap_rows;
   const float* fork_init;
+  // pipelined fork with the v channels' causal conv (width 4) + SiLU in the state waves: the v rows
+  // read are the conv's inputs; weights [Hv * Dv, 4] (the v channels' rows; bf16, or fp32 in the
+  // kernel's fp32-weight instantiation) and bias [Hv * Dv] of the same dtype, or null. t_first: the
+  // sequence row of the launch's first row (the history before sequence row 0 is zero).
+  const void* vconv_w;
+  const void* vconv_b;
+  int t_first;
+  // the v channels' conv tails (the clean raw rows before each block, [B * nb, tails_cd, 3] from the
+  // first v channel on), or null
+  void* vtails;
+  int tails_cd;
 };
 
 // Linear workgroup id such that consecutive ids run on the same XCD (dispatch is round-robin over
@@ -829,7 +840,13 @@ struct PipeSmem {
   static constexpr int O_AF = O_VP + 2 * VPB;
   static constexpr int O_TF = O_AF + 2 * FB;
   static constexpr int O_YF = O_TF + 2 * FB;
-  static constexpr int O_FLAG = O_YF + 2 * YB;  // count of state waves done reading a tile's rows
+  // v conv: per state wave, its 32 columns' weights [32][4] and bias [32] in fp32, and the carry:
+  // the clean stream's last three raw v rows before the tile, [3][32] bf16
+  static constexpr int CWB = 32 * 5 * 4;
+  static constexpr int CRB = 3 * 32 * 2;
+  static constexpr int O_CW = O_YF + 2 * YB;
+  static constexpr int O_CR = O_CW + 4 * CWB;
+  static constexpr int O_FLAG = O_CR + 4 * CRB;  // count of state waves done reading a tile's rows
   static constexpr int TOTAL = O_FLAG + 16;
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
 };
@@ -866,8 +883,12 @@ __device__ __forceinline__ void report_status(unsigned bit) {
 // NS = 1: the same kernel over one stream (the chunked rule with per-chunk states, no fork): waves
 // 6 and 7 keep the barrier sequence only, the state waves form the clean stream's products alone,
 // and the state starts from a.init ([B, Hv, 128, 128] fp32) when it is given.
-template <bool SPLIT, int NS = 2>
+// VC (two streams; 1: bf16 conv weights, 2: fp32): the v rows are the short conv's inputs, and each
+// state wave convolves its own columns of a tile's v rows in place (width 4, SiLU) before it reads
+// them, in the conv kernel's arithmetic: the layer's conv then only writes the q and k channels.
+template <bool SPLIT, int NS = 2, int VC = 0>
 __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
+  static_assert(VC == 0 || NS == 2, "the v conv runs with both streams");
   using SM = PipeSmem;
   using F = Frag<true>;
   constexpr int KT = 4;
@@ -905,6 +926,8 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   auto AFf = [&](int s) { return (float*)(smem + SM::O_AF + s * SM::FB); };
   auto TFf = [&](int s) { return (float*)(smem + SM::O_TF + s * SM::FB); };
   auto YFf = [&](int s) { return (float*)(smem + SM::O_YF + s * SM::YB); };
+  auto CWf = [&](int w) { return (float*)(smem + SM::O_CW + w * SM::CWB); };
+  auto CRf = [&](int w) { return (bf16*)(smem + SM::O_CR + w * SM::CRB); };
 
   // ---- prep waves: loads. The P wave of each stream (wave 5 / 7) loads that stream's q, k and v
   // rows, so that the G waves, whose preparation chain is the longest, issue no row loads: lane
@@ -1275,6 +1298,115 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) S[kt][v] = ip[(32 * kt + v) * 128];
   }
+  if constexpr (VC) {
+    // this wave's conv weights and bias, and the carry before the first tile: the clean stream's
+    // raw v rows t_first - 3 .. t_first - 1 of its columns (zero before the sequence start)
+    if (!idle) {
+      float* const cw = CWf(u);
+      bf16* const cr = CRf(u);
+      if (lane < 32) {
+        const long long ch = (long long)hv * 128 + cu + lane;  // v channel
+        float w4[4], bias = 0.f;
+        if (VC == 2) {
+          const float* wp = (const float*)a.vconv_w + ch * 4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w4[j] = wp[j];
+          if (a.vconv_b) bias = ((const float*)a.vconv_b)[ch];
+        } else {
+          const bf16* wp = (const bf16*)a.vconv_w + ch * 4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w4[j] = (float)wp[j];
+          if (a.vconv_b) bias = (float)((const bf16*)a.vconv_b)[ch];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cw[4 * lane + j] = w4[j];
+        cw[128 + lane] = bias;
+      }
+      const bf16* const vb = (const bf16*)a.s[0].v + b * a.v_sb + (long long)hv * a.v_sh + cu;
+      for (int i = lane; i < 96; i += 64) {
+        const int r = i >> 5, col = i & 31;
+        cr[i] = a.t_first - 3 + r >= 0 ? vb[(r - 3) * a.v_st + col] : (bf16)0.f;
+      }
+    }
+  }
+  // VC: the conv of this wave's columns of tile c's v rows, both streams, in place. Lane (p, g)
+  // takes columns cu + 2p, +1 of rows 8g .. 8g + 7; the three rows before the tile are the carry
+  // (every tile is one block, and the noised block starts from the clean rows before it), which
+  // then moves on to this tile's last three clean rows. Rows >= sub stay zero. vconv_read takes
+  // every raw value this lane needs; other lanes overwrite some of them in vconv_write, so a
+  // compiler fence must separate the two (LDS keeps one wave's accesses in order).
+  unsigned xr[2][11], nc = 0;
+  f32x4 wa, wb;
+  float ba, bb;
+  auto vconv_read = [&](int c, int pc) {
+    const int p = lane & 15, g = lane >> 4;
+    const bf16* const cr = CRf(u);
+    if (a.vtails && lane < 48) {
+      // the carry is this block's conv tails: elements 2 lane, +1 of the wave's [32 channels][3]
+      const int e0 = 2 * lane, e1 = e0 + 1;
+      const unsigned t0 = __builtin_bit_cast(unsigned short, cr[32 * (e0 % 3) + e0 / 3]);
+      const unsigned t1 = __builtin_bit_cast(unsigned short, cr[32 * (e1 % 3) + e1 / 3]);
+      const long long row = (long long)b * a.snap_rows + a.t_first / a.sub + c;
+      *(unsigned*)((bf16*)a.vtails + (row * a.tails_cd + hv * 128 + cu) * 3 + e0) = t0 | (t1 << 16);
+    }
+    const float* const cw = CWf(u);
+    wa = *(const f32x4*)(cw + 8 * p);
+    wb = *(const f32x4*)(cw + 8 * p + 4);
+    ba = cw[128 + 2 * p];
+    bb = cw[129 + 2 * p];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const bf16* const vb = VB(s, pc) + cu + 2 * p;
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        xr[s][i] = *(const unsigned*)(g == 0 ? cr + 32 * i + 2 * p : vb + (8 * g - 3 + i) * QROW);
+#pragma unroll
+      for (int i = 3; i < 11; ++i) xr[s][i] = *(const unsigned*)(vb + (8 * g + i - 3) * QROW);
+    }
+    if (g < 3) {
+      const int q = a.sub - 3 + g;  // the carry's row g for the next tile
+      nc = *(const unsigned*)(q >= 0 ? VB(0, pc) + cu + 2 * p + q * QROW : cr + 32 * (q + 3) + 2 * p);
+    }
+  };
+  // the two columns' values rounded to bf16 together (one packed conversion), as a bf16 pair
+  auto pack_bf16 = [](float x0, float x1) -> unsigned {
+    const f32x2 v = {x0, x1};
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
+  };
+  auto vconv_write = [&](int pc) {
+    const int p = lane & 15, g = lane >> 4;
+    unsigned out[2][8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        float acc0 = ba, acc1 = bb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const unsigned x = xr[s][r + j];
+          acc0 = __builtin_fmaf(wa[j], __builtin_bit_cast(float, x << 16), acc0);
+          acc1 = __builtin_fmaf(wb[j], __builtin_bit_cast(float, x & 0xffff0000u), acc1);
+        }
+        if (VC == 1) {  // bf16 weights: the sum is rounded to bf16 before the SiLU
+          const unsigned rr = pack_bf16(acc0, acc1);
+          acc0 = __builtin_bit_cast(float, rr << 16);
+          acc1 = __builtin_bit_cast(float, rr & 0xffff0000u);
+        }
+        out[s][r] = pack_bf16(silu_f32(acc0), silu_f32(acc1));
+      }
+    if (a.sub < 32) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (8 * g + r >= a.sub) out[s][r] = 0u;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) *(unsigned*)(VB(s, pc) + cu + 2 * p + (8 * g + r) * QROW) = out[s][r];
+    if (g < 3) *(unsigned*)(CRf(u) + 32 * g + 2 * p) = nc;
+  };
   for (int c = -1; c < ntiles; ++c) {
     __syncthreads();  // tile c-1's state phase and tile c's preparation are done
     if (idle) {  // the other half's columns: count as done reading the tile's rows
@@ -1308,6 +1440,12 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
       }
       // K S and Q S of both streams from the clean state before the tile; the K and Q fragments
       // of slice kt + 1 are read while the products of slice kt run
+      if constexpr (VC) {
+        vconv_read(c, pc);
+        asm volatile("" ::: "memory");  // every raw value read before any lane writes its outputs
+        vconv_write(pc);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       f32x16 accKS[NS], accQS[NS];
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -1472,15 +1610,15 @@ static int device_cus() {
 // 2: always (dllm_set_fork_split, for tests)
 static std::atomic<int> g_fork_split{0};
 
-template <int NS>
+template <int NS, int VC = 0>
 static int launch_fork_pipe(const GdnArgs& a, hipStream_t st) {
   const long long heads = (long long)a.B * a.Hv;
   const int mode = g_fork_split.load(std::memory_order_relaxed);
   const bool split = mode == 2 || (mode == 0 && 2 * heads <= device_cus());
   const long long nblk = split ? 2 * heads : heads;
   if (nblk > 0x7fffffff) return fail(DLLM_EUNSUPPORTED, "gdn: grid too large");
-  if (split) gdn_fork_pipe_kernel<true, NS><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
-  else gdn_fork_pipe_kernel<false, NS><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  if (split) gdn_fork_pipe_kernel<true, NS, VC><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
+  else gdn_fork_pipe_kernel<false, NS, VC><<<dim3((unsigned)nblk), dim3(512), 0, st>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(DLLM_ELAUNCH, "gdn fork launch: %s", hipGetErrorString(e));
   return DLLM_OK;
@@ -1599,11 +1737,30 @@ extern "C" int dllm_gdn_chunk_fwd(const void* q, const int64_t* q_strides, const
 
 // The state fork over blocks [kb0, kb1) of every sequence (the whole sequence: [0, L / block)).
 // A range after the first block starts from states[:, kb0 - 1] and runs the pipelined kernel only.
+// VConv (optional): the v channels come unconvolved from raw0 / rawt (same strides as qkv) and the
+// kernel applies the width-4 conv + SiLU to them (weights [conv_dim, 4] of dtype_w, bias or null).
+struct VConv {
+  const void* raw0;
+  const void* rawt;
+  const void* weight;
+  const void* bias;
+  int dtype_w;
+  void* tails;  // [B * nb, conv_dim, 3] (the v channels are written) or null
+  int conv_dim;
+};
+
 static int state_fork(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, int64_t qkv_stride_t,
                       const float* beta0, const float* betat, const float* g0, const float* gt, void* out0,
                       void* outt, float* states, int B, int L, int Hk, int Hv, int Dk, int Dv, int block, int dtype,
-                      float scale, int kb0, int kb1, void* stream) {
+                      float scale, int kb0, int kb1, void* stream, const VConv* vc = nullptr) {
   if (!qkv0 || !qkvt || !beta0 || !betat || !g0 || !gt || !out0 || !outt) return fail(DLLM_EINVAL, "gdn fork: null pointer");
+  if (vc) {
+    if (!vc->raw0 || !vc->rawt || !vc->weight) return fail(DLLM_EINVAL, "gdn fork v conv: null pointer");
+    if (vc->dtype_w != DT_BF16 && vc->dtype_w != DT_F32)
+      return fail(DLLM_EUNSUPPORTED, "gdn fork v conv: weight dtype %d (bf16 or fp32)", vc->dtype_w);
+    if (!(dtype == DT_BF16 && Dk == 128 && Dv == 128))
+      return fail(DLLM_EUNSUPPORTED, "gdn fork v conv: needs the pipelined kernel (bf16, Dk = Dv = 128)");
+  }
   if (B <= 0 || L <= 0 || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0 || block <= 0)
     return fail(DLLM_EINVAL, "gdn fork: bad sizes");
   if (L % block) return fail(DLLM_EINVAL, "L=%d is not a multiple of block=%d", L, block);
@@ -1620,6 +1777,11 @@ static int state_fork(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, 
   const int esz = dtype == DT_BF16 ? 2 : 4;
   const long long t_off = (long long)kb0 * block;  // first row of the range
   const char* base[2] = {(const char*)qkv0 + t_off * qkv_stride_t * esz, (const char*)qkvt + t_off * qkv_stride_t * esz};
+  const char* vbase[2] = {base[0], base[1]};
+  if (vc) {
+    vbase[0] = (const char*)vc->raw0 + t_off * qkv_stride_t * esz;
+    vbase[1] = (const char*)vc->rawt + t_off * qkv_stride_t * esz;
+  }
   const float* bet[2] = {beta0 + t_off * Hv, betat + t_off * Hv};
   const float* gg[2] = {g0 + t_off * Hv, gt + t_off * Hv};
   void* outs[2] = {(char*)out0 + t_off * Hv * Dv * esz, (char*)outt + t_off * Hv * Dv * esz};
@@ -1627,7 +1789,7 @@ static int state_fork(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, 
     GdnStream& s = a.s[i];
     s.q = base[i];
     s.k = base[i] + (long long)Hk * Dk * esz;
-    s.v = base[i] + 2LL * Hk * Dk * esz;
+    s.v = vbase[i] + 2LL * Hk * Dk * esz;
     s.beta = bet[i];
     s.g = gg[i];
     s.out = outs[i];
@@ -1657,7 +1819,25 @@ static int state_fork(const void* qkv0, const void* qkvt, int64_t qkv_stride_b, 
                      ((long long)Hk * Dk % vel == 0);
   const int dkw = Dk <= 64 ? 64 : 128;
   a.vec_qk = aligned16(qkv0) && aligned16(qkvt) && st_ok && Dk == dkw;
-  a.vec_v = aligned16(qkv0) && aligned16(qkvt) && st_ok && (Dv % window_for(dtype) == 0);
+  a.vec_v = aligned16(vbase[0]) && aligned16(vbase[1]) && st_ok && (Dv % window_for(dtype) == 0);
+  a.t_first = (int)t_off;
+  if (vc) {
+    if (!(a.vec_qk && a.vec_v))
+      return fail(DLLM_EUNSUPPORTED, "gdn fork v conv: needs 16-byte aligned rows and strides");
+    const long long wrow = 2LL * Hk * Dk;  // the first v channel's weight row
+    const int wsz = vc->dtype_w == DT_F32 ? 4 : 2;
+    a.vconv_w = (const char*)vc->weight + wrow * 4 * wsz;
+    a.vconv_b = vc->bias ? (const char*)vc->bias + wrow * wsz : nullptr;
+    if (vc->tails) {
+      if ((uintptr_t)vc->tails % 4 || vc->conv_dim % 2 || vc->conv_dim < wrow + (long long)Hv * Dv)
+        return fail(DLLM_EINVAL, "gdn fork v conv: tails need 4-byte alignment and an even conv_dim >= %lld",
+                    wrow + (long long)Hv * Dv);
+      a.vtails = (char*)vc->tails + wrow * 3 * esz;
+      a.tails_cd = vc->conv_dim;
+    }
+    return vc->dtype_w == DT_F32 ? launch_fork_pipe<2, 2>(a, (hipStream_t)stream)
+                                 : launch_fork_pipe<2, 1>(a, (hipStream_t)stream);
+  }
   // full 128 x 128 heads with 16-byte rows: the pipelined kernel
   if (dtype == DT_BF16 && Dk == 128 && Dv == 128 && a.vec_qk && a.vec_v) return launch_fork_pipe<2>(a, (hipStream_t)stream);
   if (!whole) return fail(DLLM_EUNSUPPORTED, "gdn fork: block ranges need the pipelined kernel (bf16, Dk = Dv = 128)");
@@ -1680,6 +1860,19 @@ extern "C" int dllm_gdn_state_fork_range_fwd(const void* qkv0, const void* qkvt,
                                              float scale, int block_begin, int block_end, void* stream) {
   return state_fork(qkv0, qkvt, qkv_stride_b, qkv_stride_t, beta0, betat, g0, gt, out0, outt, states, B, L, Hk, Hv,
                     Dk, Dv, block, dtype, scale, block_begin, block_end, stream);
+}
+
+extern "C" int dllm_gdn_state_fork_vconv_range_fwd(const void* qk0, const void* qkt, const void* raw0,
+                                                   const void* rawt, int64_t stride_b, int64_t stride_t,
+                                                   const void* conv_weight, const void* conv_bias, int dtype_w,
+                                                   void* conv_tails, int conv_dim, const float* beta0,
+                                                   const float* betat, const float* g0, const float* gt, void* out0,
+                                                   void* outt, float* states, int B, int L, int Hk, int Hv, int Dk,
+                                                   int Dv, int block, int dtype, float scale, int block_begin,
+                                                   int block_end, void* stream) {
+  const VConv vc = {raw0, rawt, conv_weight, conv_bias, dtype_w, conv_tails, conv_dim};
+  return state_fork(qk0, qkt, stride_b, stride_t, beta0, betat, g0, gt, out0, outt, states, B, L, Hk, Hv, Dk, Dv,
+                    block, dtype, scale, block_begin, block_end, stream, &vc);
 }
 
 extern "C" int dllm_set_fork_split(int mode) {

@@ -46,6 +46,13 @@ _SIGNATURES = {
         _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p, _c_fp, _c_fp, _c_void_p, _c_void_p,
         _c_fp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int,
         _c_void_p]),
+    "dllm_gdn_state_fork_vconv_range_fwd": (_c_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p, _c_int, _c_void_p,
+        _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_fp, _c_int, _c_int,
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int, _c_void_p]),
+    "dllm_conv_fork_channels_range_fwd": (_c_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "dllm_conv_fork_fwd": (_c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p]),

@@ -219,7 +219,7 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
                    num_k_heads: int, num_v_heads: int, head_k_dim: int, head_v_dim: int, block: int,
                    conv_bias: torch.Tensor | None = None, need_states: bool = True,
                    need_tails: bool = True, fault: str | None = None, out: dict | None = None,
-                   pieces: int | None = None):
+                   pieces: int | None = None, vconv: bool | None = None):
     """The state-fork GDN layer core on pre-conv projections of both streams
     (reference blockdiff.py:153-177 with gdn.py:217-231, projections excluded).
 
@@ -235,7 +235,11 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     range before it (each fork range starts from the snapshot the one before wrote), which needs
     the pipelined fork kernel and the states. None (default) takes 4 ranges where that applies and
     the fork's grid leaves compute units free for the conv, else 1. Every schedule returns the same
-    results bit for bit."""
+    results bit for bit.
+
+    vconv: the v channels' conv inside the fork kernel (the conv launch then convolves only the q
+    and k channels, and the v channels of y0/yt are left unwritten). None (default) takes it where
+    it measured faster (vconv_pays); True requires it. Results are bit-identical either way."""
     dev = _lib.require_device(raw0, rawt, conv_weight, beta0, betat, g0, gt, conv_bias)
     if raw0.shape != rawt.shape or raw0.dim() != 3:
         raise ValueError("raw0 and rawt must both be [B, L, conv_dim]")
@@ -281,6 +285,14 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     # block ranges run on the pipelined kernel, which reads 16-byte rows of the conv outputs
     ranges_ok = (states is not None and nb >= 2 and Lb.dllm_gdn_state_fork_path(Dk, Dv, block, code) == 2
                  and y0.data_ptr() % 16 == 0 and yt.data_ptr() % 16 == 0)
+    vc_ok = (vconv_supported(Lb, K, Dk, Dv, block, code) and fault is None
+             and all(t.data_ptr() % 16 == 0 for t in (r0, rt, y0, yt)))
+    if vconv is None:
+        vconv = vc_ok and vconv_pays(_device_cus(dev), B, Hv)
+    elif vconv and not vc_ok:
+        raise ValueError("vconv needs the pipelined fork kernel (bf16, Dk = Dv = 128, block dividing 32), a width-4 "
+                         "conv, 16-byte aligned buffers and no fault")
+    vconv = bool(vconv)
     if pieces is None:
         pieces = default_pieces(_device_cus(dev), B, Hv, nb) if ranges_ok else 1
     pieces = int(pieces)
@@ -293,8 +305,15 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
         pieces = min(pieces, nb)
         cuts = [nb * i // pieces for i in range(pieces + 1)]
         _launch_ranges(Lb, dev, cuts, (r0, rt, w, bias, y0, yt, tails, cflags),
-                       (y0, yt, b0, bt_, gg0, ggt, o0, ot, states), (B, L, Cd, K, Hk, Hv, Dk, Dv, block, code))
-        _IMPL["last"], _IMPL["reason"] = "hip", f"pipelined fork kernel, {pieces} block ranges beside the conv"
+                       (y0, yt, b0, bt_, gg0, ggt, o0, ot, states), (B, L, Cd, K, Hk, Hv, Dk, Dv, block, code),
+                       vconv=vconv)
+        _IMPL["last"], _IMPL["reason"] = "hip", (f"pipelined fork kernel{' with the v conv' if vconv else ''}, "
+                                                 f"{pieces} block ranges beside the conv")
+        return {"o0": o0, "ot": ot, "states": states, "tails": tails, "y0": y0, "yt": yt}
+    if vconv:
+        _launch_vconv(Lb, sh, 0, nb, (r0, rt, w, bias, y0, yt, tails),
+                      (b0, bt_, gg0, ggt, o0, ot, states), (B, L, Cd, K, Hk, Hv, Dk, Dv, block, code))
+        _IMPL["last"], _IMPL["reason"] = "hip", "pipelined fork kernel with the v conv"
         return {"o0": o0, "ot": ot, "states": states, "tails": tails, "y0": y0, "yt": yt}
     _lib.check(Lb.dllm_conv_fork_fwd(
         r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(bias), y0.data_ptr(), yt.data_ptr(),
@@ -361,6 +380,38 @@ def default_pieces(cus: int, B: int, Hv: int, nb: int) -> int:
     return 1
 
 
+def vconv_supported(Lb, K: int, Dk: int, Dv: int, block: int, code: int) -> bool:
+    """Whether the fork kernel can take the v channels' conv: the pipelined kernel (bf16,
+    Dk = Dv = 128, a block dividing 32) and a width-4 conv."""
+    return K == 4 and Lb.dllm_gdn_state_fork_path(Dk, Dv, block, code) == 2
+
+
+def vconv_pays(cus: int, B: int, Hv: int) -> bool:
+    """Whether the v conv inside the fork measured faster than the conv launch doing it: with one
+    fork workgroup per (sequence, head) (27B-class layer, B = 4, L = 4096: 0.771 vs 0.825 ms per
+    step after 30 warm-ups, 0.856 vs 0.891 ms under 5; bit-identical), not with a head's columns
+    split over two workgroups, where half the state waves carry it (0.8B-class: 414 vs 406 us)."""
+    return fork_workgroups(cus, B, Hv) == B * Hv
+
+
+def _launch_vconv(Lb, sh, k0, k1, conv, fork, dims):
+    """Blocks [k0, k1) of the layer with the v conv inside the fork: the conv launch over the q and
+    k channels (their y and tails), then the fork reading the v channels' raw rows (writing their
+    tails), both on stream handle `sh`."""
+    r0, rt, w, bias, y0, yt, tails = conv
+    b0, bt_, gg0, ggt, o0, ot, states = fork
+    B, L, Cd, K, Hk, Hv, Dk, Dv, block, code = dims
+    wcode = _lib.dtype_code(w.dtype)
+    _lib.check(Lb.dllm_conv_fork_channels_range_fwd(
+        r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(bias), y0.data_ptr(), yt.data_ptr(), _lib.ptr(tails),
+        B, L, Cd, K, block, code, wcode, 0, k0, k1, 2 * Hk * Dk, sh), "dllm_conv_fork_channels_range_fwd")
+    _lib.check(Lb.dllm_gdn_state_fork_vconv_range_fwd(
+        y0.data_ptr(), yt.data_ptr(), r0.data_ptr(), rt.data_ptr(), L * Cd, Cd, w.data_ptr(), _lib.ptr(bias), wcode,
+        _lib.ptr(tails), Cd, b0.data_ptr(), bt_.data_ptr(), gg0.data_ptr(), ggt.data_ptr(), o0.data_ptr(),
+        ot.data_ptr(), _lib.ptr(states), B, L, Hk, Hv, Dk, Dv, block, code, Dk ** -0.5, k0, k1, sh),
+        "dllm_gdn_state_fork_vconv_range_fwd")
+
+
 def _side_stream(dev: torch.device) -> torch.cuda.Stream:
     """This thread's side stream on `dev` (default priority), created once."""
     streams = getattr(_SIDE, "streams", None)
@@ -372,7 +423,7 @@ def _side_stream(dev: torch.device) -> torch.cuda.Stream:
     return streams[idx]
 
 
-def _launch_ranges(Lb, dev, cuts, conv, fork, dims):
+def _launch_ranges(Lb, dev, cuts, conv, fork, dims, vconv=False):
     """The layer in block ranges [cuts[i], cuts[i+1]): every conv range on this thread's side
     stream, in order, each followed by an event; each fork range on the current stream after its
     conv range's event, starting from the snapshot the range before wrote (the kernels' arithmetic
@@ -385,15 +436,25 @@ def _launch_ranges(Lb, dev, cuts, conv, fork, dims):
     side.wait_stream(main)  # the inputs as the caller's stream leaves them
     wcode = _lib.dtype_code(w.dtype)
     events = []
+    # with vconv: the conv ranges cover the q and k channels; each fork range convolves its v rows
+    # (reading the three raw rows before the range) and writes their tails
+    yc = 2 * Hk * Dk if vconv else Cd
     for k0, k1 in zip(cuts, cuts[1:]):
-        _lib.check(Lb.dllm_conv_fork_range_fwd(
+        _lib.check(Lb.dllm_conv_fork_channels_range_fwd(
             r0.data_ptr(), rt.data_ptr(), w.data_ptr(), _lib.ptr(bias), y0.data_ptr(), yt.data_ptr(), _lib.ptr(tails),
-            B, L, Cd, K, block, code, wcode, cflags, k0, k1, side.cuda_stream), "dllm_conv_fork_range_fwd")
+            B, L, Cd, K, block, code, wcode, cflags, k0, k1, yc, side.cuda_stream), "dllm_conv_fork_channels_range_fwd")
         ev = torch.cuda.Event()
         ev.record(side)
         events.append(ev)
     for ev, (k0, k1) in zip(events, zip(cuts, cuts[1:])):
         main.wait_event(ev)
+        if vconv:
+            _lib.check(Lb.dllm_gdn_state_fork_vconv_range_fwd(
+                c0.data_ptr(), ct.data_ptr(), r0.data_ptr(), rt.data_ptr(), L * Cd, Cd, w.data_ptr(), _lib.ptr(bias),
+                wcode, _lib.ptr(tails), Cd, b0.data_ptr(), bt_.data_ptr(), gg0.data_ptr(), ggt.data_ptr(),
+                o0.data_ptr(), ot.data_ptr(), _lib.ptr(states), B, L, Hk, Hv, Dk, Dv, block, code, Dk ** -0.5, k0,
+                k1, main.cuda_stream), "dllm_gdn_state_fork_vconv_range_fwd")
+            continue
         _lib.check(Lb.dllm_gdn_state_fork_range_fwd(
             c0.data_ptr(), ct.data_ptr(), L * Cd, Cd, b0.data_ptr(), bt_.data_ptr(), gg0.data_ptr(), ggt.data_ptr(),
             o0.data_ptr(), ot.data_ptr(), _lib.ptr(states), B, L, Hk, Hv, Dk, Dv, block, code, Dk ** -0.5, k0, k1,
@@ -471,7 +532,7 @@ class StateForkPlan:
     at construction (their contents may be rewritten between runs)."""
 
     def __init__(self, raw0, rawt, conv_weight, beta0, betat, g0, gt, *, num_k_heads, num_v_heads, head_k_dim,
-                 head_v_dim, block, need_states=True, need_tails=True):
+                 head_v_dim, block, need_states=True, need_tails=True, vconv=None):
         dev = _lib.require_device(raw0, rawt, conv_weight, beta0, betat, g0, gt)
         B, L, Cd = raw0.shape
         self.dims = (B, L, Cd, num_k_heads, num_v_heads, head_k_dim, head_v_dim, block)
@@ -496,10 +557,24 @@ class StateForkPlan:
                        if need_states else None)
         self.device = dev
         self._lib = _lib.lib()
+        # the v channels' conv inside the fork (gdn_state_fork's vconv): None takes it where it pays
+        ok = (vconv_supported(self._lib, K, head_k_dim, head_v_dim, block, self.code)
+              and raw0.data_ptr() % 16 == 0 and rawt.data_ptr() % 16 == 0)
+        if vconv is None:
+            vconv = ok and vconv_pays(_device_cus(dev), B, num_v_heads)
+        elif vconv and not ok:
+            raise ValueError("vconv needs the pipelined fork kernel (bf16, Dk = Dv = 128) and a width-4 conv")
+        self.vconv = bool(vconv)
 
     def run_conv(self, stream=None):
         B, L, Cd, Hk, Hv, Dk, Dv, block = self.dims
         sh = stream if stream is not None else _lib.stream_handle(self.device)
+        if self.vconv:  # the q and k channels only; the fork convolves the v channels
+            _lib.check(self._lib.dllm_conv_fork_channels_range_fwd(
+                self.raw0.data_ptr(), self.rawt.data_ptr(), self.w.data_ptr(), None, self.y0.data_ptr(),
+                self.yt.data_ptr(), _lib.ptr(self.tails), B, L, Cd, self.K, block, self.code,
+                _lib.dtype_code(self.w.dtype), 0, 0, L // block, 2 * Hk * Dk, sh), "dllm_conv_fork_channels_range_fwd")
+            return
         _lib.check(self._lib.dllm_conv_fork_fwd(
             self.raw0.data_ptr(), self.rawt.data_ptr(), self.w.data_ptr(), None, self.y0.data_ptr(),
             self.yt.data_ptr(), _lib.ptr(self.tails), B, L, Cd, self.K, block, self.code,
@@ -508,6 +583,15 @@ class StateForkPlan:
     def run_core(self, stream=None):
         B, L, Cd, Hk, Hv, Dk, Dv, block = self.dims
         sh = stream if stream is not None else _lib.stream_handle(self.device)
+        if self.vconv:
+            _lib.check(self._lib.dllm_gdn_state_fork_vconv_range_fwd(
+                self.y0.data_ptr(), self.yt.data_ptr(), self.raw0.data_ptr(), self.rawt.data_ptr(), L * Cd, Cd,
+                self.w.data_ptr(), None, _lib.dtype_code(self.w.dtype), _lib.ptr(self.tails), Cd,
+                self.beta0.data_ptr(),
+                self.betat.data_ptr(), self.g0.data_ptr(), self.gt.data_ptr(), self.o0.data_ptr(),
+                self.ot.data_ptr(), _lib.ptr(self.states), B, L, Hk, Hv, Dk, Dv, block, self.code, Dk ** -0.5, 0,
+                L // block, sh), "dllm_gdn_state_fork_vconv_range_fwd")
+            return
         _lib.check(self._lib.dllm_gdn_state_fork_fwd(
             self.y0.data_ptr(), self.yt.data_ptr(), L * Cd, Cd, self.beta0.data_ptr(), self.betat.data_ptr(),
             self.g0.data_ptr(), self.gt.data_ptr(), self.o0.data_ptr(), self.ot.data_ptr(), _lib.ptr(self.states),
@@ -544,5 +628,5 @@ class StateForkPlan:
         _launch_ranges(self._lib, self.device, cuts,
                        (self.raw0, self.rawt, self.w, None, self.y0, self.yt, self.tails, 0),
                        (self.y0, self.yt, self.beta0, self.betat, self.g0, self.gt, self.o0, self.ot, self.states),
-                       (B, L, Cd, self.K, Hk, Hv, Dk, Dv, block, self.code))
+                       (B, L, Cd, self.K, Hk, Hv, Dk, Dv, block, self.code), vconv=self.vconv)
         _IMPL["last"], _IMPL["reason"] = "hip", ""

@@ -115,6 +115,27 @@ int dllm_set_spin_limit(int limit);
  * never splits, mode 2 always does. Results are identical either way. Process-wide; returns the
  * previous mode. For tests and measurement; no counterpart in the reference.
  */
+/*
+ * dllm_gdn_state_fork_range_fwd with the v channels' short conv done inside the fork kernel. The
+ * reference runs the conv of all channels first (src/dllm_qwen38/gdn.py:217-219 with the noised
+ * prefix cut at blockdiff.py:167-173) and then the core; here the conv launch
+ * (dllm_conv_fork_channels_range_fwd with y_channels = 2*Hk*Dk) writes only the q and k channels,
+ * and the fork reads the v channels' pre-conv rows and convolves them (width 4 + SiLU, the
+ * dllm_conv_fork_fwd arithmetic, bit for bit), which saves the v channels' round trip through HBM.
+ * qk0/qkt: the conv outputs (q and k channels read); raw0/rawt: the conv inputs (v channels read),
+ * both [B,L,conv_dim] with the strides given. conv_weight [conv_dim,4] bf16 or fp32 (dtype_w),
+ * conv_bias [conv_dim] of that dtype or NULL. conv_tails: the [B*nb,conv_dim,3] tails tensor,
+ * whose v channels this call writes for its blocks (4-byte aligned, conv_dim even), or NULL.
+ * The pipelined fork kernel only (dllm_gdn_state_fork_path() == 2; else -2). No fault flags.
+ */
+int dllm_gdn_state_fork_vconv_range_fwd(const void* qk0, const void* qkt, const void* raw0, const void* rawt,
+                                        int64_t stride_b, int64_t stride_t, const void* conv_weight,
+                                        const void* conv_bias, int dtype_w, void* conv_tails, int conv_dim,
+                                        const float* beta0, const float* betat, const float* g0,
+                                        const float* gt, void* out0, void* outt, float* states, int B, int L,
+                                        int Hk, int Hv, int Dk, int Dv, int block, int dtype, float scale,
+                                        int block_begin, int block_end, void* stream);
+
 int dllm_set_fork_split(int mode);
 /* Test only: with on != 0, the LDS row-buffer wait waits for a count that is never reached, so
  * every such wait gives up after the spin limit (the kernel still ends, outputs invalid). Returns
@@ -144,6 +165,16 @@ int dllm_conv_fork_range_fwd(const void* raw0, const void* rawt, const void* wei
                              void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
                              int block, int dtype_x, int dtype_w, int flags, int block_begin,
                              int block_end, void* stream);
+
+/*
+ * dllm_conv_fork_range_fwd over channels [0, y_channels) only (their y rows and tails; the other
+ * channels of y0, yt and tails are left untouched). For dllm_gdn_state_fork_vconv_range_fwd, which
+ * convolves the v channels itself; no counterpart in the reference. 0 <= y_channels <= conv_dim.
+ */
+int dllm_conv_fork_channels_range_fwd(const void* raw0, const void* rawt, const void* weight, const void* bias,
+                                      void* y0, void* yt, void* tails, int B, int L, int conv_dim, int width,
+                                      int block, int dtype_x, int dtype_w, int flags, int block_begin,
+                                      int block_end, int y_channels, void* stream);
 
 /*
  * Generic causal depthwise conv (+ optional SiLU) with an optional prefix.

@@ -169,7 +169,8 @@ def test_state_fork_27b_full_size_properties(dev):
     s = inputs.GDN_27B_BF16
     x = inputs.gdn_layer_inputs(s)
     xd = _to(x, dev)
-    kw = dict(num_k_heads=s.Hk, num_v_heads=s.Hv, head_k_dim=s.D, head_v_dim=s.D, block=s.block)
+    # the conv outputs' v channels are read below: the conv launch writes them (no v conv in the fork)
+    kw = dict(num_k_heads=s.Hk, num_v_heads=s.Hv, head_k_dim=s.D, head_v_dim=s.D, block=s.block, vconv=False)
     r1 = gdn.gdn_state_fork(xd["raw0"], xd["rawt"], xd["conv_w"], xd["beta0"], xd["betat"], xd["g0"], xd["gt"], **kw)
     o0a, ota, sta = r1["o0"].clone(), r1["ot"].clone(), r1["states"].clone()
     r2 = gdn.gdn_state_fork(xd["raw0"], xd["rawt"], xd["conv_w"], xd["beta0"], xd["betat"], xd["g0"], xd["gt"], **kw)

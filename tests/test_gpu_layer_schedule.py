@@ -128,7 +128,10 @@ def test_state_fork_api_schedules_are_bit_identical(dev, shape, B, L):
         ref = _fork(x, s, pieces=1, **kw)
         torch.cuda.synchronize()
         assert "block ranges" not in gdn.last_impl()[1]
-        ref = {k: v.clone() for k, v in ref.items() if v is not None}
+        # with the v conv inside the fork (the automatic choice where it pays) the conv launch
+        # leaves the v channels of y0 and yt unwritten: compare its own channels there
+        cy = 2 * s.Hk * s.D if "v conv" in gdn.last_impl()[1] else None
+        ref = {k: (v[..., :cy] if k in ("y0", "yt") else v).clone() for k, v in ref.items() if v is not None}
         for pieces in (None, 2, 3, 7):
             print(f"{shape} B={B} L={L} {sorted(kw)} pieces={pieces}", flush=True)
             got = _fork(x, s, pieces=pieces, **kw)
@@ -136,7 +139,8 @@ def test_state_fork_api_schedules_are_bit_identical(dev, shape, B, L):
             ranges = pieces is not None or auto_ranges
             assert ("block ranges" in gdn.last_impl()[1]) == ranges, (pieces, gdn.last_impl())
             for k in ref:
-                assert torch.equal(got[k], ref[k]), (kw, pieces, k)
+                g = got[k][..., :cy] if k in ("y0", "yt") else got[k]
+                assert torch.equal(g, ref[k]), (kw, pieces, k)
     assert gdn.kernel_status(reset=True) == 0
 
 

@@ -1002,7 +1002,11 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   // q and k rows (the LDS counter `flag`), tile c + 2's q and k rows into the buffers of tile c.
   // The roles run separate loops with the same barrier sequence, so that neither role's registers
   // (prefetched rows, the state) are held live through the other.
-  if (tid == 0) *flag = 0u;
+  if (tid == 0) {
+    flag[0] = 0u;  // the P waves' row-buffer count
+    flag[1] = 0u;  // column split with the v conv: tiles convolved for state waves 0 and 1
+    flag[2] = 0u;
+  }
   if constexpr (NS == 1) {
     if (prep && gs == 1) {  // no second stream: the barrier sequence of the prep loop only
       for (int c = -1; c < ntiles; ++c) __syncthreads();
@@ -1329,34 +1333,37 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
       }
     }
   }
-  // VC: the conv of this wave's columns of tile c's v rows, both streams, in place. Lane (p, g)
-  // takes columns cu + 2p, +1 of rows 8g .. 8g + 7; the three rows before the tile are the carry
-  // (every tile is one block, and the noised block starts from the clean rows before it), which
-  // then moves on to this tile's last three clean rows. Rows >= sub stay zero. vconv_read takes
-  // every raw value this lane needs; other lanes overwrite some of them in vconv_write, so a
-  // compiler fence must separate the two (LDS keeps one wave's accesses in order).
+  // VC: the conv of 32 columns [cv, cv + 32) of tile c's v rows, both streams, in place, with the
+  // weights and carry of state-wave slot w (the slot that owns those columns). Lane (p, g) takes
+  // columns cv + 2p, +1 of rows 8g .. 8g + 7; the three rows before the tile are the carry (every
+  // tile is one block, and the noised block starts from the clean rows before it), which then moves
+  // on to this tile's last three clean rows. Rows >= sub stay zero. vconv_read takes every raw value
+  // this lane needs; other lanes overwrite some of them in vconv_write, so a compiler fence must
+  // separate the two (LDS keeps one wave's accesses in order). Without the column split each state
+  // wave convolves its own columns; with it, the state waves 2 and 3, which own no columns, convolve
+  // those of waves 0 and 1 and raise a per-slot LDS counter that waves 0 and 1 wait for.
   unsigned xr[2][11], nc = 0;
   f32x4 wa, wb;
   float ba, bb;
-  auto vconv_read = [&](int c, int pc) {
+  auto vconv_read = [&](int c, int pc, int cv, int w) {
     const int p = lane & 15, g = lane >> 4;
-    const bf16* const cr = CRf(u);
+    const bf16* const cr = CRf(w);
     if (a.vtails && lane < 48) {
       // the carry is this block's conv tails: elements 2 lane, +1 of the wave's [32 channels][3]
       const int e0 = 2 * lane, e1 = e0 + 1;
       const unsigned t0 = __builtin_bit_cast(unsigned short, cr[32 * (e0 % 3) + e0 / 3]);
       const unsigned t1 = __builtin_bit_cast(unsigned short, cr[32 * (e1 % 3) + e1 / 3]);
       const long long row = (long long)b * a.snap_rows + a.t_first / a.sub + c;
-      *(unsigned*)((bf16*)a.vtails + (row * a.tails_cd + hv * 128 + cu) * 3 + e0) = t0 | (t1 << 16);
+      *(unsigned*)((bf16*)a.vtails + (row * a.tails_cd + hv * 128 + cv) * 3 + e0) = t0 | (t1 << 16);
     }
-    const float* const cw = CWf(u);
+    const float* const cw = CWf(w);
     wa = *(const f32x4*)(cw + 8 * p);
     wb = *(const f32x4*)(cw + 8 * p + 4);
     ba = cw[128 + 2 * p];
     bb = cw[129 + 2 * p];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const bf16* const vb = VB(s, pc) + cu + 2 * p;
+      const bf16* const vb = VB(s, pc) + cv + 2 * p;
 #pragma unroll
       for (int i = 0; i < 3; ++i)
         xr[s][i] = *(const unsigned*)(g == 0 ? cr + 32 * i + 2 * p : vb + (8 * g - 3 + i) * QROW);
@@ -1365,7 +1372,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
     }
     if (g < 3) {
       const int q = a.sub - 3 + g;  // the carry's row g for the next tile
-      nc = *(const unsigned*)(q >= 0 ? VB(0, pc) + cu + 2 * p + q * QROW : cr + 32 * (q + 3) + 2 * p);
+      nc = *(const unsigned*)(q >= 0 ? VB(0, pc) + cv + 2 * p + q * QROW : cr + 32 * (q + 3) + 2 * p);
     }
   };
   // the two columns' values rounded to bf16 together (one packed conversion), as a bf16 pair
@@ -1373,7 +1380,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
     const f32x2 v = {x0, x1};
     return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
   };
-  auto vconv_write = [&](int pc) {
+  auto vconv_write = [&](int pc, int cv, int w) {
     const int p = lane & 15, g = lane >> 4;
     unsigned out[2][8];
 #pragma unroll
@@ -1404,13 +1411,27 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int r = 0; r < 8; ++r) *(unsigned*)(VB(s, pc) + cu + 2 * p + (8 * g + r) * QROW) = out[s][r];
-    if (g < 3) *(unsigned*)(CRf(u) + 32 * g + 2 * p) = nc;
+      for (int r = 0; r < 8; ++r) *(unsigned*)(VB(s, pc) + cv + 2 * p + (8 * g + r) * QROW) = out[s][r];
+    if (g < 3) *(unsigned*)(CRf(w) + 32 * g + 2 * p) = nc;
+  };
+  auto vconv = [&](int c, int pc, int cv, int w) {
+    vconv_read(c, pc, cv, w);
+    asm volatile("" ::: "memory");  // every raw value read before any lane writes its outputs
+    vconv_write(pc, cv, w);
   };
   for (int c = -1; c < ntiles; ++c) {
     __syncthreads();  // tile c-1's state phase and tile c's preparation are done
     if (idle) {  // the other half's columns: count as done reading the tile's rows
       if (c >= 0 && lane == 0) __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if constexpr (VC != 0) {
+        if (c >= 0) {
+          // the conv of state wave (u & 1)'s columns, then its counter (after the LDS writes land)
+          const int w = u & 1;
+          vconv(c, c & 1, half * 64 + w * 32, w);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (lane == 0) __hip_atomic_fetch_add(flag + 1 + w, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+      }
       continue;
     }
     if (c >= 0) {
@@ -1440,10 +1461,8 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
       }
       // K S and Q S of both streams from the clean state before the tile; the K and Q fragments
       // of slice kt + 1 are read while the products of slice kt run
-      if constexpr (VC) {
-        vconv_read(c, pc);
-        asm volatile("" ::: "memory");  // every raw value read before any lane writes its outputs
-        vconv_write(pc);
+      if constexpr (VC != 0 && !SPLIT) {
+        vconv(c, pc, cu, u);
         __builtin_amdgcn_sched_barrier(0);
       }
       f32x16 accKS[NS], accQS[NS];
@@ -1488,6 +1507,20 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
       for (int kt = 0; kt < KT; ++kt) lds_frag_tr_d(KB(0, pc) + kt * 32, QROW, lane, fku[kt]);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (lane == 0) __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if constexpr (VC != 0 && SPLIT) {
+        // this wave's columns of the v rows are convolved by state wave u + 2: wait for its count
+        // (bounded; it never waits on this wave inside a phase)
+        const unsigned target = (unsigned)(c + 1) + (unsigned)a.wait_bias;
+        for (int spin = 0;; ++spin) {
+          if (__hip_atomic_load(flag + 1 + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+          if (spin >= a.spin_limit) {
+            if (lane == 0) report_status(STATUS_LDS_WAIT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("" ::: "memory");
+      }
       // V' = U - T1 (K S) = T2 V + (-T1) (K S): W = T1 K is never formed; K S feeds straight back
       // as the B operand of the -T1 product (its rows are the tile rows in rho order)
       f32x16 accV[NS];

@@ -238,8 +238,11 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     results bit for bit.
 
     vconv: the v channels' conv inside the fork kernel (the conv launch then convolves only the q
-    and k channels, and the v channels of y0/yt are left unwritten). None (default) takes it where
-    it measured faster (vconv_pays); True requires it. Results are bit-identical either way."""
+    and k channels, and the v channels of y0/yt are left unwritten), which saves their round trip
+    through HBM. None (default) takes it wherever the pipelined kernel runs and there is no fault;
+    True requires it. Results are bit-identical either way. Measured (step medians, interleaved):
+    the 27B-class layer (B = 4, L = 4096) 0.740 vs 0.819 ms, the 0.8B-class layer (B = 8,
+    L = 2048, a head's columns over two workgroups) 381 vs 405 us."""
     dev = _lib.require_device(raw0, rawt, conv_weight, beta0, betat, g0, gt, conv_bias)
     if raw0.shape != rawt.shape or raw0.dim() != 3:
         raise ValueError("raw0 and rawt must both be [B, L, conv_dim]")
@@ -288,7 +291,7 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     vc_ok = (vconv_supported(Lb, K, Dk, Dv, block, code) and fault is None
              and all(t.data_ptr() % 16 == 0 for t in (r0, rt, y0, yt)))
     if vconv is None:
-        vconv = vc_ok and vconv_pays(_device_cus(dev), B, Hv)
+        vconv = vc_ok
     elif vconv and not vc_ok:
         raise ValueError("vconv needs the pipelined fork kernel (bf16, Dk = Dv = 128, block dividing 32), a width-4 "
                          "conv, 16-byte aligned buffers and no fault")
@@ -384,14 +387,6 @@ def vconv_supported(Lb, K: int, Dk: int, Dv: int, block: int, code: int) -> bool
     """Whether the fork kernel can take the v channels' conv: the pipelined kernel (bf16,
     Dk = Dv = 128, a block dividing 32) and a width-4 conv."""
     return K == 4 and Lb.dllm_gdn_state_fork_path(Dk, Dv, block, code) == 2
-
-
-def vconv_pays(cus: int, B: int, Hv: int) -> bool:
-    """Whether the v conv inside the fork measured faster than the conv launch doing it: with one
-    fork workgroup per (sequence, head) (27B-class layer, B = 4, L = 4096: 0.771 vs 0.825 ms per
-    step after 30 warm-ups, 0.856 vs 0.891 ms under 5; bit-identical), not with a head's columns
-    split over two workgroups, where half the state waves carry it (0.8B-class: 414 vs 406 us)."""
-    return fork_workgroups(cus, B, Hv) == B * Hv
 
 
 def _launch_vconv(Lb, sh, k0, k1, conv, fork, dims):
@@ -557,11 +552,11 @@ class StateForkPlan:
                        if need_states else None)
         self.device = dev
         self._lib = _lib.lib()
-        # the v channels' conv inside the fork (gdn_state_fork's vconv): None takes it where it pays
+        # the v channels' conv inside the fork (gdn_state_fork's vconv): None takes it where supported
         ok = (vconv_supported(self._lib, K, head_k_dim, head_v_dim, block, self.code)
               and raw0.data_ptr() % 16 == 0 and rawt.data_ptr() % 16 == 0)
         if vconv is None:
-            vconv = ok and vconv_pays(_device_cus(dev), B, num_v_heads)
+            vconv = ok
         elif vconv and not ok:
             raise ValueError("vconv needs the pipelined fork kernel (bf16, Dk = Dv = 128) and a width-4 conv")
         self.vconv = bool(vconv)

@@ -32,7 +32,10 @@ def test_overlapped_schedule_is_bit_identical(dev, shape, B, L):
     assert p.overlap_supported()
     p.run()
     torch.cuda.synchronize()
-    ref = {k: getattr(p, k).clone() for k in OUTS}
+    # with the v conv inside the fork the conv launches write only the q and k channels of y0, yt
+    cy = 2 * s.Hk * s.D if p.vconv else s.conv_dim
+    view = lambda k, t: t[..., :cy] if k in ("y0", "yt") else t  # noqa: E731
+    ref = {k: view(k, getattr(p, k)).clone() for k in OUTS}
     nb = L // s.block
     for kw in ({"pieces": 2}, {"pieces": 3}, {"pieces": 5}, {"bounds": [0, 1, nb // 2, nb]},
                {"bounds": [0, nb - 1, nb]}):
@@ -42,7 +45,7 @@ def test_overlapped_schedule_is_bit_identical(dev, shape, B, L):
         p.run_overlapped(**kw)
         torch.cuda.synchronize()
         for k in OUTS:
-            assert torch.equal(getattr(p, k), ref[k]), (kw, k)
+            assert torch.equal(view(k, getattr(p, k)), ref[k]), (kw, k)
     assert gdn.kernel_status(reset=True) == 0
 
 
@@ -177,7 +180,10 @@ def test_ranges_at_subtile_blocks_are_bit_identical(dev, block):
     assert p.overlap_supported()
     p.run()
     torch.cuda.synchronize()
-    ref = {k: getattr(p, k).clone() for k in OUTS}
+    # with the v conv inside the fork the conv launches write only the q and k channels of y0, yt
+    cy = 2 * s.Hk * s.D if p.vconv else s.conv_dim
+    view = lambda k, t: t[..., :cy] if k in ("y0", "yt") else t  # noqa: E731
+    ref = {k: view(k, getattr(p, k)).clone() for k in OUTS}
     for kw in ({"pieces": 3}, {"bounds": [0, 1, nb // 2 + 1, nb]}):
         for k in OUTS:
             getattr(p, k).fill_(float("nan"))
@@ -185,13 +191,13 @@ def test_ranges_at_subtile_blocks_are_bit_identical(dev, block):
         p.run_overlapped(**kw)
         torch.cuda.synchronize()
         for k in OUTS:
-            assert torch.equal(getattr(p, k), ref[k]), (kw, k)
+            assert torch.equal(view(k, getattr(p, k)), ref[k]), (kw, k)
     x = {k: v.to(dev) for k, v in inputs.gdn_layer_inputs(s, B=B, L=L, g_shift=-4.0).items()}
     one = _fork(x, s, pieces=1)
     torch.cuda.synchronize()
-    one = {k: v.clone() for k, v in one.items() if v is not None}
+    one = {k: view(k, v).clone() for k, v in one.items() if v is not None}
     got = _fork(x, s, pieces=5)
     torch.cuda.synchronize()
     for k in one:
-        assert torch.equal(got[k], one[k]), k
+        assert torch.equal(view(k, got[k]), one[k]), k
     assert gdn.kernel_status(reset=True) == 0

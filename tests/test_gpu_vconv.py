@@ -7,11 +7,13 @@ the clean and noised outputs, the fp32 snapshots, the conv tails (the fork write
 tails) and the q and k channels of the conv outputs.
 
 Cases: the 27B-class benchmark layer at full size; the 0.8B-class layer at full size (its heads
-split over two workgroups, so only two state waves per workgroup convolve); blocks 32 down to 1,
-where a tile has fewer real rows than the conv history (the carry then spans several tiles); fp32
-conv weights (no rounding before the SiLU); a conv bias; slow decay; block ranges, whose fork
-launches start from the raw rows before the range; without snapshots or tails. The fork with the
-v conv is also compared with the fp32 CPU oracle (the 27B-class layer, in test_gpu_fullsize)."""
+split over two workgroups: there the two state waves that own no columns convolve those of the
+other two, which wait for a per-wave LDS count; every small case below runs this layout too);
+blocks 32 down to 1, where a tile has fewer real rows than the conv history (the carry then spans
+several tiles); fp32 conv weights (no rounding before the SiLU); a conv bias; slow decay; block
+ranges, whose fork launches start from the raw rows before the range; without snapshots or tails.
+The fork with the v conv is also compared with the fp32 CPU oracle (here at small sizes, and the
+27B- and 0.8B-class layers at full size in test_gpu_fullsize)."""
 
 import dataclasses
 

@@ -239,10 +239,13 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
 
     vconv: the v channels' conv inside the fork kernel (the conv launch then convolves only the q
     and k channels, and the v channels of y0/yt are left unwritten), which saves their round trip
-    through HBM. None (default) takes it wherever the pipelined kernel runs and there is no fault;
-    True requires it. Results are bit-identical either way. Measured (step medians, interleaved):
-    the 27B-class layer (B = 4, L = 4096) 0.740 vs 0.819 ms, the 0.8B-class layer (B = 8,
-    L = 2048, a head's columns over two workgroups) 381 vs 405 us."""
+    through HBM. None (default) takes it where the pipelined kernel runs, there is no fault and the
+    states are kept; True requires it. Results are bit-identical either way. Measured (step
+    medians, interleaved): the 27B-class layer (B = 4, L = 4096) 0.740 vs 0.819 ms, the 0.8B-class
+    layer (B = 8, L = 2048, a head's columns over two workgroups) 381 vs 405 us. Without the
+    states the fork is bound by its tile chain rather than by its stores, so the conv's arithmetic
+    costs it more than the conv launch saves (the 16-layer stack's layers, B = 1, L = 2048: fork
+    258 vs 224 us, conv 19 vs 34 us)."""
     dev = _lib.require_device(raw0, rawt, conv_weight, beta0, betat, g0, gt, conv_bias)
     if raw0.shape != rawt.shape or raw0.dim() != 3:
         raise ValueError("raw0 and rawt must both be [B, L, conv_dim]")
@@ -291,7 +294,7 @@ def gdn_state_fork(raw0: torch.Tensor, rawt: torch.Tensor, conv_weight: torch.Te
     vc_ok = (vconv_supported(Lb, K, Dk, Dv, block, code) and fault is None
              and all(t.data_ptr() % 16 == 0 for t in (r0, rt, y0, yt)))
     if vconv is None:
-        vconv = vc_ok
+        vconv = vc_ok and states is not None
     elif vconv and not vc_ok:
         raise ValueError("vconv needs the pipelined fork kernel (bf16, Dk = Dv = 128, block dividing 32), a width-4 "
                          "conv, 16-byte aligned buffers and no fault")
@@ -553,10 +556,11 @@ class StateForkPlan:
         self.device = dev
         self._lib = _lib.lib()
         # the v channels' conv inside the fork (gdn_state_fork's vconv): None takes it where supported
+        # and the states are kept
         ok = (vconv_supported(self._lib, K, head_k_dim, head_v_dim, block, self.code)
               and raw0.data_ptr() % 16 == 0 and rawt.data_ptr() % 16 == 0)
         if vconv is None:
-            vconv = ok
+            vconv = ok and need_states
         elif vconv and not ok:
             raise ValueError("vconv needs the pipelined fork kernel (bf16, Dk = Dv = 128) and a width-4 conv")
         self.vconv = bool(vconv)

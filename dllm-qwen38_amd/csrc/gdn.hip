@@ -1383,8 +1383,12 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   auto vconv_write = [&](int pc, int cv, int w) {
     const int p = lane & 15, g = lane >> 4;
     unsigned out[2][8];
+    // per stream: the sums, then the SiLU (silu_f32's steps) in stages over all 16 values, so that
+    // the exponentials and reciprocals of different values follow each other instead of each
+    // waiting on its own (no hazard wait states; 0.8B-class fork 282 vs 285 us, bit-identical)
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < 2; ++s) {
+      float a0[8], a1[8], e0[8], e1[8];
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         float acc0 = ba, acc1 = bb;
@@ -1399,8 +1403,22 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           acc0 = __builtin_bit_cast(float, rr << 16);
           acc1 = __builtin_bit_cast(float, rr & 0xffff0000u);
         }
-        out[s][r] = pack_bf16(silu_f32(acc0), silu_f32(acc1));
+        a0[r] = acc0;
+        a1[r] = acc1;
       }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        e0[r] = __builtin_amdgcn_exp2f(-1.4426950408889634f * a0[r]);
+        e1[r] = __builtin_amdgcn_exp2f(-1.4426950408889634f * a1[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        e0[r] = __builtin_amdgcn_rcpf(1.0f + e0[r]);
+        e1[r] = __builtin_amdgcn_rcpf(1.0f + e1[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) out[s][r] = pack_bf16(a0[r] * e0[r], a1[r] * e1[r]);
+    }
     if (a.sub < 32) {
 #pragma unroll
       for (int s = 0; s < 2; ++s)

@@ -844,7 +844,10 @@ struct PipeSmem {
   // the clean stream's last three raw v rows before the tile, [3][32] bf16
   static constexpr int CWB = 32 * 5 * 4;
   static constexpr int CRB = 3 * 32 * 2;
-  static constexpr int O_CW = O_YF + 2 * YB;
+  // G-wave column factors per stream: beta_i / ||k_i|| and beta e^gamma / ||k|| (32 floats each)
+  static constexpr int VGB = 2 * 32 * 4;
+  static constexpr int O_VG = O_YF + 2 * YB;
+  static constexpr int O_CW = O_VG + 2 * VGB;
   static constexpr int O_CR = O_CW + 4 * CWB;
   static constexpr int O_FLAG = O_CR + 4 * CRB;  // count of state waves done reading a tile's rows
   static constexpr int TOTAL = O_FLAG + 16;
@@ -854,6 +857,7 @@ struct PipeSmem {
 enum { VS_EGQ = 0, VS_RNK = 32, VS_EGLK = 64, VS_EG = 96 };
 enum { VA_GAML = 0, VA_BET = 32, VA_EG = 64, VA_EGL = 96 };
 enum { VP_GAML = 0, VP_EG = 32 };
+enum { VG_BR = 0, VG_C1 = 32 };
 
 // Bit of the library's per-device status word (dllm_status): the bounded LDS row-buffer wait of
 // the pipelined fork gave up (the launch's outputs are then invalid).
@@ -926,6 +930,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
   auto AFf = [&](int s) { return (float*)(smem + SM::O_AF + s * SM::FB); };
   auto TFf = [&](int s) { return (float*)(smem + SM::O_TF + s * SM::FB); };
   auto YFf = [&](int s) { return (float*)(smem + SM::O_YF + s * SM::YB); };
+  auto VGf = [&](int s) { return (float*)(smem + SM::O_VG + s * SM::VGB); };
   auto CWf = [&](int w) { return (float*)(smem + SM::O_CW + w * SM::CWB); };
   auto CRf = [&](int w) { return (bf16*)(smem + SM::O_CR + w * SM::CRB); };
 
@@ -1077,26 +1082,28 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           // of row l32; the row's 1/||k|| goes to the state vectors and comes back as row vectors
           const float rj = a.l2norm ? rsqrtf(row_sumsq(fa) + 1e-6f) : 1.f;
           const float eglj = va[VA_EGL + l32];
+          float* const vg = VGf(gs);
           if (h == 0) {
             vs[VS_EGLK + l32] = eglj * rj;
             vs[VS_RNK + l32] = rj;
             vs[VS_EG + l32] = va[VA_EG + l32];
+            // per-row factors of A and T1, formed once per row instead of once per element (the
+            // same products in the same order)
+            const float bet = va[VA_BET + l32];
+            vg[VG_BR + l32] = bet * rj;
+            vg[VG_C1 + l32] = bet * va[VA_EG + l32] * rj;
           }
           wave_lds_sync();
           const float gj = va[VA_GAML + l32];
-          f32x4 bet4[4], rnk4[4];
+          f32x4 br4[4];
 #pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            bet4[m] = *(const f32x4*)(va + VA_BET + 8 * m + 4 * h);
-            rnk4[m] = *(const f32x4*)(vs + VS_RNK + 8 * m + 4 * h);
-          }
+          for (int m = 0; m < 4; ++m) br4[m] = *(const f32x4*)(vg + VG_BR + 8 * m + 4 * h);
 #pragma unroll
           for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int i = 8 * m + 4 * h + e;
-              const float val = (bet4[m][e] * rnk4[m][e] * rj) * acc[4 * m + e] *
-                                __builtin_amdgcn_exp2f(gam4[m][e] - gj);
+              const float val = (br4[m][e] * rj) * acc[4 * m + e] * __builtin_amdgcn_exp2f(gam4[m][e] - gj);
               AF[i * FROW + l32] = (lo < 8 * m + 4 * ho + e) ? val : 0.f;
             }
           wave_lds_sync();
@@ -1128,70 +1135,71 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
             }
           }
           wave_lds_sync();
-          // level 1: T[m+1][m] = -D[m+1] (A[m+1][m] D[m]) for the three sub-diagonal 8x8 blocks
+          // level 1: T[m+1][m] = -D[m+1] (A[m+1][m] D[m]) for the sub-diagonal 8x8 blocks m = 0 and 2
+          // (inside the 16x16 diagonal blocks; the block m = 1 lies in T[16:32][0:16], which level 2
+          // writes whole without reading it)
           {
             const int ii = lane >> 3, jj = lane & 7;
-            f32x4 arow[3][2];
-            float dcol[3][8];
+            f32x4 arow[2][2];
+            float dcol[2][8];
 #pragma unroll
-            for (int m = 0; m < 3; ++m) {
-              arow[m][0] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m);
-              arow[m][1] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m + 4);
+            for (int q = 0; q < 2; ++q) {
+              const int m = 2 * q;
+              arow[q][0] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m);
+              arow[q][1] = *(const f32x4*)(AF + (8 * (m + 1) + ii) * FROW + 8 * m + 4);
 #pragma unroll
-              for (int kk = 0; kk < 8; ++kk) dcol[m][kk] = TF[(8 * m + kk) * FROW + 8 * m + jj];
+              for (int kk = 0; kk < 8; ++kk) dcol[q][kk] = TF[(8 * m + kk) * FROW + 8 * m + jj];
             }
 #pragma unroll
-            for (int m = 0; m < 3; ++m) {
+            for (int q = 0; q < 2; ++q) {
               float sacc = 0.f;
 #pragma unroll
-              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(arow[m][kk >> 2][kk & 3], dcol[m][kk], sacc);
-              YF[m * 64 + ii * 8 + jj] = sacc;
+              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(arow[q][kk >> 2][kk & 3], dcol[q][kk], sacc);
+              YF[q * 64 + ii * 8 + jj] = sacc;
             }
             wave_lds_sync();
-            f32x4 drow[3][2];
-            float ycol[3][8];
+            f32x4 drow[2][2];
+            float ycol[2][8];
 #pragma unroll
-            for (int m = 0; m < 3; ++m) {
-              drow[m][0] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1));
-              drow[m][1] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1) + 4);
+            for (int q = 0; q < 2; ++q) {
+              const int m = 2 * q;
+              drow[q][0] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1));
+              drow[q][1] = *(const f32x4*)(TF + (8 * (m + 1) + ii) * FROW + 8 * (m + 1) + 4);
 #pragma unroll
-              for (int kk = 0; kk < 8; ++kk) ycol[m][kk] = YF[m * 64 + kk * 8 + jj];
+              for (int kk = 0; kk < 8; ++kk) ycol[q][kk] = YF[q * 64 + kk * 8 + jj];
             }
 #pragma unroll
-            for (int m = 0; m < 3; ++m) {
+            for (int q = 0; q < 2; ++q) {
+              const int m = 2 * q;
               float sacc = 0.f;
 #pragma unroll
-              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(drow[m][kk >> 2][kk & 3], ycol[m][kk], sacc);
+              for (int kk = 0; kk < 8; ++kk) sacc = __builtin_fmaf(drow[q][kk >> 2][kk & 3], ycol[q][kk], sacc);
               TF[(8 * (m + 1) + ii) * FROW + 8 * m + jj] = -sacc;
             }
           }
           wave_lds_sync();
-          // level 2: T[16:32][0:16] = -T22 (A21 T11), lane -> row 16 + i2, columns j2..j2+3
+          // level 2: T[16:32][0:16] = -T22 (A21 T11) as fp32 16x16x4 matrix products (lane l supplies
+          // A[l % 16][l / 16] and B[l / 16][l % 16] and holds D[4 (l / 16) + v][l % 16]), the
+          // intermediate through YF; on the VALU this level was 128 FMAs per lane, on a SIMD whose
+          // VALU the state wave beside it needs (27B-class fork 623 vs 649 us; the outputs measured
+          // bit-identical to the FMA form, whose sums ran in the same k order)
           {
-            const int i2 = lane >> 2, j2 = (lane & 3) * 4;
-            f32x4 arow[4], tcol[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) arow[q] = *(const f32x4*)(AF + (16 + i2) * FROW + 4 * q);
-#pragma unroll
-            for (int kk = 0; kk < 16; ++kk) tcol[kk] = *(const f32x4*)(TF + kk * FROW + j2);
+            const int li = lane & 15, lk = lane >> 4;
             f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 16; ++kk)
+            for (int kb = 0; kb < 4; ++kb)
+              y = __builtin_amdgcn_mfma_f32_16x16x4f32(AF[(16 + li) * FROW + 4 * kb + lk], TF[(4 * kb + lk) * FROW + li], y,
+                                                       0, 0, 0);
 #pragma unroll
-              for (int e = 0; e < 4; ++e) y[e] = __builtin_fmaf(arow[kk >> 2][kk & 3], tcol[kk][e], y[e]);
-            *(f32x4*)(YF + i2 * 20 + j2) = y;
+            for (int v = 0; v < 4; ++v) YF[(4 * lk + v) * 20 + li] = y[v];
             wave_lds_sync();
-            f32x4 trow[4], ycol[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) trow[q] = *(const f32x4*)(TF + (16 + i2) * FROW + 16 + 4 * q);
-#pragma unroll
-            for (int kk = 0; kk < 16; ++kk) ycol[kk] = *(const f32x4*)(YF + kk * 20 + j2);
             f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 16; ++kk)
+            for (int kb = 0; kb < 4; ++kb)
+              z = __builtin_amdgcn_mfma_f32_16x16x4f32(TF[(16 + li) * FROW + 16 + 4 * kb + lk], YF[(4 * kb + lk) * 20 + li],
+                                                       z, 0, 0, 0);
 #pragma unroll
-              for (int e = 0; e < 4; ++e) z[e] = __builtin_fmaf(trow[kk >> 2][kk & 3], ycol[kk][e], z[e]);
-            *(f32x4*)(TF + (16 + i2) * FROW + j2) = -z;
+            for (int v = 0; v < 4; ++v) TF[(16 + 4 * lk + v) * FROW + li] = -z[v];
           }
           wave_lds_sync();
           // T1 = T diag(beta e^gamma / ||k||) and T2 = T diag(beta) as operand fragments
@@ -1201,12 +1209,11 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           for (int m = 0; m < 4; ++m) {
             const f32x4 t4 = *(const f32x4*)(TF + l32 * FROW + 8 * m + 4 * h);
             const f32x4 be4 = *(const f32x4*)(va + VA_BET + 8 * m + 4 * h);
-            const f32x4 eg4 = *(const f32x4*)(va + VA_EG + 8 * m + 4 * h);
-            const f32x4 rk4 = *(const f32x4*)(vs + VS_RNK + 8 * m + 4 * h);
+            const f32x4 c14 = *(const f32x4*)(vg + VG_C1 + 8 * m + 4 * h);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const bool in = 8 * m + 4 * ho + e <= lo;
-              tv1[4 * m + e] = in ? -(t4[e] * (be4[e] * eg4[e] * rk4[e])) : 0.f;  // -T1
+              tv1[4 * m + e] = in ? -(t4[e] * c14[e]) : 0.f;  // -T1
               tv2[4 * m + e] = in ? t4[e] * be4[e] : 0.f;
             }
           }

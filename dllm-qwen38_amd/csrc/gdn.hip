@@ -871,8 +871,33 @@ static __device__ unsigned dllm_status_word;
 // the fork 559.6 vs 594.3 us with the compiler's non-temporal store (571.2 us for the same nt
 // store issued this way, 562.3 us with system scope), bit-identical; 253.1 vs 259.2 us at the
 // 0.8B-class layer.
-__device__ __forceinline__ void store_snapshot(float* p, float v) {
-  asm volatile("global_store_dword %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+// OFF: an immediate byte offset from p.
+template <int OFF> __device__ __forceinline__ void store_snapshot(float* p, float v) {
+  asm volatile("global_store_dword %0, %1, off offset:%2 nt sc1" ::"v"(p), "v"(v), "i"(OFF) : "memory");
+}
+// The 16 values of one 32-row slice of a state wave's accumulator: rows 32 kt + 16 h + v of the
+// snapshot (p0 = row 32 kt + 16 h), 512 bytes apart, as immediate offsets from two base addresses
+// (v < 8 and v >= 8) instead of an address formed per store. With the v conv on the state waves
+// (whose VALU is then the bound) this measured 604 vs 611 us at the 27B-class fork and 260 vs
+// 270 us at the 0.8B-class, bit-identical (before it: 581 vs 561 us, slower).
+__device__ __forceinline__ void store_snapshot_slice(float* p0, const f32x16& s) {
+  float* const p1 = p0 + 8 * 128;
+  store_snapshot<0>(p0, s[0]);
+  store_snapshot<512>(p0, s[1]);
+  store_snapshot<1024>(p0, s[2]);
+  store_snapshot<1536>(p0, s[3]);
+  store_snapshot<2048>(p0, s[4]);
+  store_snapshot<2560>(p0, s[5]);
+  store_snapshot<3072>(p0, s[6]);
+  store_snapshot<3584>(p0, s[7]);
+  store_snapshot<0>(p1, s[8]);
+  store_snapshot<512>(p1, s[9]);
+  store_snapshot<1024>(p1, s[10]);
+  store_snapshot<1536>(p1, s[11]);
+  store_snapshot<2048>(p1, s[12]);
+  store_snapshot<2560>(p1, s[13]);
+  store_snapshot<3072>(p1, s[14]);
+  store_snapshot<3584>(p1, s[15]);
 }
 
 __device__ __forceinline__ void report_status(unsigned bit) {
@@ -1628,10 +1653,7 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) S[kt][v] *= lam;
             mma32(S[kt], fku[kt], fd);
-            if (sb) {
-#pragma unroll
-              for (int v = 0; v < 16; ++v) store_snapshot(sb + (32 * kt + v) * 128, S[kt][v]);
-            }
+            if (sb) store_snapshot_slice(sb + 32 * kt * 128, S[kt]);
           }
         }
       }

@@ -1621,7 +1621,11 @@ __global__ __launch_bounds__(512) void gdn_fork_pipe_kernel(GdnArgs a) {
           // the 16-byte stores at the start of the next phase; rows >= sub are staged but not stored
           bf16* const st = VB(s, pc) + cu + l32 + 4 * h * QROW;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) st[(((v >> 2) << 3) + (v & 3)) * QROW] = (bf16)accQS[s][v];
+          for (int v = 0; v < 16; v += 2) {  // two values per conversion; rows rho(v), rho(v + 1)
+            const unsigned pr = pack_bf16(accQS[s][v], accQS[s][v + 1]);
+            *(unsigned short*)(st + (((v >> 2) << 3) + (v & 3)) * QROW) = (unsigned short)pr;
+            *(unsigned short*)(st + ((((v + 1) >> 2) << 3) + ((v + 1) & 3)) * QROW) = (unsigned short)(pr >> 16);
+          }
         } else {
           // the last tile of the launch: straight to the outputs
           bf16* ob = (bf16*)a.s[s].out + ((long long)b * a.t_rows + t0) * rs + (long long)hv * a.Dv + cu;

@@ -58,6 +58,18 @@ def conv(raw0=P, B=1, L=64, Cd=64, width=4, block=32, dx=BF, dw=BF, rng=None):
     return ("dllm_conv_fork_range_fwd", *head, rng[0], rng[1], None)
 
 
+def vfork(qk=P, raw=P, w=P, dtw=BF, tails=P, cd=768, B=1, L=64, Hk=2, Hv=2, Dk=128, Dv=128, block=32, dtype=BF,
+          stride_t=768):
+    """dllm_gdn_state_fork_vconv_range_fwd over the whole sequence."""
+    return ("dllm_gdn_state_fork_vconv_range_fwd", qk, P, raw, P, stride_t * L, stride_t, w, None, dtw, tails, cd,
+            P, P, P, P, P, P, P, B, L, Hk, Hv, Dk, Dv, block, dtype, 0.088, 0, max(1, L // block), None)
+
+
+def convc(yc, Cd=64):
+    """dllm_conv_fork_channels_range_fwd over blocks [0, 2) with y_channels = yc."""
+    return ("dllm_conv_fork_channels_range_fwd", P, P, P, None, P, P, P, 1, 64, Cd, 4, 32, BF, BF, 0, 0, 2, yc, None)
+
+
 def conv1d(x=P, B=1, C=64, T=16, width=4, prefix=None, plen=0, dx=BF, dw=BF):
     return ("dllm_causal_conv1d_fwd", x, s3(T * C, C, 1), prefix, s3(3 * C, 3, 1) if plen else None, plen, P, None,
             P, B, C, T, width, dx, dw, 1, None)
@@ -251,6 +263,17 @@ CASES = {
     # 512 workgroups over 3200 units of 80 k-steps split tiles: 512 x 2 pieces of 16 KB > 8 MiB
     "noalloc past the array": (("dllm_decode_linear_fwd_noalloc", P, P, P, 32, 5120, 5120, 512, BF, None), EUNSUP,
                                "more than the 8388608-byte array"),
+    # the fork with the v channels' conv inside, and the conv over the q and k channels only
+    "vconv null raw rows": (vfork(raw=None), EINVAL, "gdn fork v conv: null pointer"),
+    "vconv weight dtype": (vfork(dtw=7), EUNSUP, "weight dtype 7"),
+    "vconv head dim 64": (vfork(Dk=64, Dv=64, stride_t=384), EUNSUP, "needs the pipelined kernel"),
+    "vconv fp32": (vfork(dtype=F32), EUNSUP, "needs the pipelined kernel"),
+    "vconv misaligned raw rows": (vfork(raw=P2), EUNSUP, "16-byte aligned rows and strides"),
+    "vconv misaligned tails": (vfork(tails=P2), EINVAL, "tails need 4-byte alignment"),
+    "vconv odd conv_dim": (vfork(cd=767), EINVAL, "tails need 4-byte alignment and an even conv_dim"),
+    "vconv block range": (vfork() [:-3] + (1, 1, None), EINVAL, "block range [1, 1)"),
+    "conv channels past conv_dim": (convc(128), EINVAL, "y_channels 128 > conv_dim 64"),
+    "conv channels negative": (convc(-1), EINVAL, "y_channels -1 < 0"),
     # fork layout (src/dllm_qwen38/blockdiff.py:161-177)
     "layout prefix missing": (("dllm_fork_layout", 1, 64, 32, 4, P, P, None, None), EINVAL, "fork layout: null pointer"),
     "layout width 0": (("dllm_fork_layout", 1, 64, 32, 0, P, P, P, None), EINVAL, "fork layout: bad sizes"),

@@ -86,17 +86,19 @@ def test_vconv_equals_conv_then_fork(dev, name, s, opt):
     _assert_same(got, ref, s, name)
 
 
-@pytest.mark.parametrize("B,L", [(1, 512), (4, 2048)])
-def test_vconv_block_ranges(dev, B, L):
+@pytest.mark.parametrize("B,L,block,small", [(1, 512, 32, False), (4, 2048, 32, False), (2, 64, 2, True),
+                                              (2, 128, 8, True)])
+def test_vconv_block_ranges(dev, B, L, block, small):
     """Ranges with the v conv: each fork range reads the three raw rows before it as the conv
-    history and starts from the snapshot the range before wrote; equal to one unfused launch."""
-    s = dataclasses.replace(inputs.GDN_27B_BF16, B=B, L=L, g_shift=-4.0)
+    history (at block 2 they span two blocks) and starts from the snapshot the range before wrote;
+    equal to one unfused launch."""
+    s = dataclasses.replace(SMALL if small else inputs.GDN_27B_BF16, B=B, L=L, block=block, g_shift=-4.0)
     x, extra = _inputs(dev, s, bias=True)
     ref = _fork(x, s, vconv=False, pieces=1, **extra)
     torch.cuda.synchronize()
     ref = {k: v.clone() for k, v in ref.items()}
     for pieces in (2, 3, 7):
-        print(f"B={B} L={L} vconv pieces={pieces}", flush=True)
+        print(f"B={B} L={L} block={block} vconv pieces={pieces}", flush=True)
         got = _fork(x, s, vconv=True, pieces=pieces, **extra)
         torch.cuda.synchronize()
         assert "v conv" in gdn.last_impl()[1] and "block ranges" in gdn.last_impl()[1], gdn.last_impl()

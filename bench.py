@@ -3,9 +3,10 @@
 Workload (one step = one layer call on one batch): B=4, L=4096, block = chunk = 32 (128 noised
 rows per sequence), 16 key heads / 48 value heads, d_k = d_v = 128, conv width 4, bf16 with fp32
 state and accumulation; synthetic seeded inputs already resident in HBM. A step runs the two HIP
-kernels of the layer: the two-stream causal conv with conv-prefix carry-in, and the fused
-chunked delta rule (intra-chunk UT transform, sequential state pass with per-block fp32 state
-snapshots, every noised block relaunched from its clean-prefix state).
+kernels of the layer: the two-stream causal conv of the q and k channels with conv-prefix
+carry-in, and the fused chunked delta rule, which convolves the v channels itself as their rows
+arrive (intra-chunk UT transform, sequential state pass with per-block fp32 state snapshots,
+every noised block relaunched from its clean-prefix state).
 
 tokens = B*L clean positions per layer call (each carries its noised twin).
 
